@@ -1,0 +1,202 @@
+"""ctypes binding of libbitmamba_hip.so (the C ABI declared in include/bm_hip.h).
+
+Python callers (tests, bench.py) reach the gfx950 kernels only through this
+module.  Loading fails loudly when the library has not been built; there is
+no CPU fallback.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbitmamba_hip.so")
+
+_vp, _sz, _i, _f, _u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_float, C.c_uint64
+_fp = C.POINTER(C.c_float)
+_i8p = C.POINTER(C.c_int8)
+_u8p = C.POINTER(C.c_uint8)
+
+
+class Tensor(C.Structure):
+    """struct tensor (src/bitmamba.h:65-74)."""
+    _fields_ = [("data", _fp), ("packed_data", _u8p), ("rows", _i), ("cols", _i),
+                ("n_elements", _sz), ("is_bitnet", C.c_bool), ("scale", _f)]
+
+
+class SynthConfig(C.Structure):
+    _fields_ = [("vocab", _i), ("d_model", _i), ("n_layers", _i), ("n_heads", _i),
+                ("in_proj_rows", _i), ("ternary_dist", _i), ("fp_sigma", _f),
+                ("ternary_scale", _f), ("seed", _u64)]
+
+
+class Dispatch(C.Structure):
+    """Layout mirror of kernel_dispatch_t (src/dispatch.h:87-95)."""
+    _fields_ = [("rms_norm", _vp), ("bitlinear_forward", _vp),
+                ("bitlinear_forward_batch", _vp), ("bitlinear_prepare", _vp),
+                ("bitlinear_row_worker", _vp), ("ssm_inner", _vp), ("name", C.c_char_p)]
+
+
+# name -> (restype, argtypes); every symbol of include/bm_hip.h
+SIGNATURES = {
+    "bm_hip_init": (C.c_bool, []),
+    "bm_hip_available": (C.c_bool, []),
+    "bm_hip_set_mmap": (C.c_bool, [_vp, _sz]),
+    "bm_hip_cleanup": (None, []),
+    "bm_hip_last_error": (C.c_char_p, []),
+    "hip_rms_norm": (_f, [_vp, _i, _vp, _vp]),
+    "hip_bitlinear_forward": (None, [_vp, _i, C.POINTER(Tensor), C.POINTER(Tensor), _vp, _vp, _vp]),
+    "hip_bitlinear_forward_batch": (None, [_vp, _i, _i, C.POINTER(Tensor), C.POINTER(Tensor),
+                                           _vp, _vp, _vp, _i]),
+    "bm_hip_register": (C.c_bool, [C.POINTER(Dispatch)]),
+    "bm_hip_bitlinear_forward_batch": (None, [_vp, _i, _i, _vp, _i, _i, _f, _vp, _vp, _vp,
+                                              _vp, _i]),
+    "bm_hip_malloc": (_vp, [_sz]),
+    "bm_hip_free": (None, [_vp]),
+    "bm_hip_memcpy_h2d": (_i, [_vp, _vp, _sz]),
+    "bm_hip_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "bm_hip_memset": (_i, [_vp, _i, _sz]),
+    "bm_hip_synchronize": (_i, []),
+    "bm_hip_canonicalize_dev": (_i, [_vp, _sz, _vp]),
+    "bm_hip_act_bytes": (_sz, [_i, _i]),
+    "bm_hip_quantize_dev": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
+    "bm_hip_bitlinear_act_dev": (_i, [_vp, _vp, _i, _vp, _i, _i, _f, _i, _vp, _vp]),
+    "bm_hip_bitlinear_dev": (_i, [_vp, _i, _i, _vp, _vp, _i, _f, _i, _vp, _vp, _i, _vp, _vp,
+                                  _vp]),
+    "bm_hip_i8_act_bytes": (_sz, [_i, _i]),
+    "bm_hip_ternary_gemm_i32_dev": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "bm_bit2_synth_size": (_sz, [C.POINTER(SynthConfig)]),
+    "bm_bit2_synth_write": (_i, [C.POINTER(SynthConfig), _vp, _sz]),
+    "bm_synth_ternary": (None, [_u64, _i, _i, _i, _i, _vp]),
+    "bm_synth_normal": (None, [_u64, _i, _sz, _f, _vp]),
+    "bm_synth_int8": (None, [_u64, _i, _sz, _vp]),
+    "bm_synth_prompt": (None, [_u64, _i, _i, _vp]),
+}
+
+SYNTH_UNIFORM, SYNTH_P0_40, SYNTH_P0_60, SYNTH_RAW_BYTES = 0, 1, 2, 3
+
+_lib = None
+
+
+def lib():
+    """The loaded library with argtypes set (raises if it was never built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("%s is not built; run __graft_entry__.build()" % LIB_PATH)
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return (lib().bm_hip_last_error() or b"").decode()
+
+
+def ptr(a):
+    return a.ctypes.data_as(_vp)
+
+
+def check(rc, what="call"):
+    if rc != 0:
+        raise RuntimeError("%s failed (%d): %s" % (what, rc, last_error()))
+
+
+# ---------------------------------------------------------------------------
+# synthetic data (host side, no GPU needed)
+# ---------------------------------------------------------------------------
+def synth_ternary(seed, tensor, rows, cols, dist=SYNTH_UNIFORM):
+    out = np.empty((rows, (cols + 3) // 4), dtype=np.uint8)
+    lib().bm_synth_ternary(seed, tensor, rows, cols, dist, ptr(out))
+    return out
+
+
+def synth_normal(seed, tensor, shape, sigma=1.0):
+    out = np.empty(shape, dtype=np.float32)
+    lib().bm_synth_normal(seed, tensor, out.size, sigma, ptr(out))
+    return out
+
+
+def synth_int8(seed, tensor, shape):
+    out = np.empty(shape, dtype=np.int8)
+    lib().bm_synth_int8(seed, tensor, out.size, ptr(out))
+    return out
+
+
+def synth_prompt(seed, vocab, n):
+    out = np.empty(n, dtype=np.int32)
+    lib().bm_synth_prompt(seed, vocab, n, ptr(out))
+    return out
+
+
+def synth_model(vocab, d_model, n_layers, n_heads, seed, dist=SYNTH_UNIFORM, fp_sigma=0.02,
+                ternary_scale=0.02, in_proj_rows=0):
+    cfg = SynthConfig(vocab, d_model, n_layers, n_heads, in_proj_rows, dist, fp_sigma,
+                      ternary_scale, seed)
+    n = lib().bm_bit2_synth_size(C.byref(cfg))
+    if n == 0:
+        raise ValueError("invalid synthetic model config")
+    buf = np.empty(n, dtype=np.uint8)
+    check(lib().bm_bit2_synth_write(C.byref(cfg), ptr(buf), n), "bm_bit2_synth_write")
+    return buf
+
+
+# ---------------------------------------------------------------------------
+# device buffers
+# ---------------------------------------------------------------------------
+class DeviceBuffer:
+    """A device allocation owned by the library's allocator."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().bm_hip_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise MemoryError("bm_hip_malloc(%d): %s" % (self.nbytes, last_error()))
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().bm_hip_memcpy_h2d(self.ptr, ptr(a), a.nbytes), "h2d")
+
+    def download(self, shape, dtype):
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        check(lib().bm_hip_memcpy_d2h(ptr(out), self.ptr, out.nbytes), "d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().bm_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def make_tensor(packed=None, rows=0, cols=0, scale=1.0, data=None):
+    t = Tensor()
+    if packed is not None:
+        t.packed_data = packed.ctypes.data_as(_u8p)
+        t.is_bitnet = True
+        t.rows, t.cols, t.scale = rows, cols, scale
+        t.n_elements = rows * cols
+    if data is not None:
+        t.data = data.ctypes.data_as(_fp)
+        t.rows = data.shape[0]
+        t.n_elements = data.size
+        t.scale = 1.0
+    return t

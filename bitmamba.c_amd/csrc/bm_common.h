@@ -1,0 +1,63 @@
+// Internal definitions shared by the HIP translation units of the BitLinear
+// backend (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+// Activation workspace written by the quantizer for each token (row of
+// act_row_bytes(K) bytes, 256-byte aligned):
+//   [0, 4*S)            int32 sum of the token's int8 values per 1024-column
+//                       slice (S = ceil(K/1024)), used for w = code - 1
+//   [nib_off, +K)       split-nibble copy for the v_dot8 GEMV: per 16 columns
+//                       four dwords {lo4(even cols), lo4(odd), hi4(even),
+//                       hi4(odd)}; nibble n of "even" is column 2n
+//   [perm_off, +K)      int8 copy for the MFMA GEMM: per 16 columns, byte
+//                       4k+b holds column 4b+k (the order in which a packed
+//                       dword decodes to four int8 dwords)
+namespace bm {
+
+constexpr int kSlice = 1024;  // scalar T-MAC block: 256 groups of 4 columns
+
+__host__ __device__ inline int slices_of(int K) { return (K + kSlice - 1) / kSlice; }
+__host__ __device__ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+__host__ __device__ inline size_t act_nib_off(int K) { return align_up((size_t)slices_of(K) * 4, 64); }
+__host__ __device__ inline size_t act_perm_off(int K) { return act_nib_off(K) + align_up((size_t)K, 64); }
+__host__ __device__ inline size_t act_row_bytes(int K) {
+  return align_up(act_perm_off(K) + align_up((size_t)K, 64), 256);
+}
+
+}  // namespace bm
+
+#define BM_HIP_CHECK_RET(expr, ret)                                            \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      bm_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),     \
+                   __FILE__, __LINE__);                                        \
+      return ret;                                                              \
+    }                                                                          \
+  } while (0)
+
+extern "C" void bm_set_error(const char *fmt, ...);
+
+// Kernel launchers (bm_kernels.hip).  All return hipSuccess or the launch
+// error; shapes are validated by the callers.
+namespace bm {
+
+hipError_t launch_quantize(const float *x, int M, int n, int x_stride,
+                           const float *gamma, float *x_norm, int8_t *xq,
+                           int quant_stride, float *scale_x, uint8_t *act,
+                           hipStream_t s);
+hipError_t launch_prep_i8(const int8_t *xq, int M, int ldx, int K, uint8_t *act,
+                          hipStream_t s);
+// fp32 output with the scalar 1024-column epilogue; inv[m] computed from
+// scale_x[m] and w_scale (scale_x == nullptr -> int32 totals into out_i32)
+hipError_t launch_product(const uint8_t *act, const float *scale_x, int M,
+                          const uint8_t *packed, int N, int K, float w_scale,
+                          bool canonical, float *out, int32_t *out_i32,
+                          hipStream_t s);
+hipError_t launch_canonicalize(uint8_t *p, size_t bytes, hipStream_t s);
+
+}  // namespace bm

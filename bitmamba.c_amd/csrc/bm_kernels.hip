@@ -1,0 +1,632 @@
+// gfx950 kernels of the ternary BitLinear hot path.
+//
+// Numerics (parity mode, the only mode): every kernel reproduces the
+// reference's scalar path bit for bit (src/kernel.c:72-129, 346-448):
+//   * sum of squares in four interleaved sequential fp32 chains, combined
+//     ((s0+s1)+s2)+s3, tail added last (src/kernel.c:77-89);
+//   * rms = 1/sqrtf(sum/n + 1e-6f), out = (x*rms)*w, no FMA contraction
+//     (the file is built with -ffp-contract=off and uses __f*_rn);
+//   * int8 = clamp((int)(v + (v >= 0 ? .5f : -.5f)), -128, 127);
+//   * int32 totals per 1024-column block, fp32 out += total*inv_scale in
+//     block order, then the K % 4 remainder (src/kernel.c:255-256, 407-447).
+// Ternary decode: code = bits, w = min(code - 1, 1) (src/quantization.c:
+// 27-31).  Kernels compute x.w = x.code - sum(x) with code in {0,1,2}; a
+// code 11 is rewritten to 10 first (same value) unless the caller promises
+// canonical weights.
+#include "bm_common.h"
+
+namespace bm {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t canon_codes(uint32_t p) {
+  // field 11 -> 10: clear the low bit where both bits are set
+  return p - (((p >> 1) & p) & 0x55555555u);
+}
+
+// ---------------------------------------------------------------------------
+// Activation workspace writers
+// ---------------------------------------------------------------------------
+
+// 16 int8 values of columns 16g..16g+15 -> split nibbles + permuted int8
+__device__ __forceinline__ void write_act_group(uint8_t* __restrict__ act_row, int K, int g,
+                                                const int (&q)[16]) {
+  uint32_t le = 0, lo = 0, he = 0, ho = 0;
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int xe = q[2 * n], xo = q[2 * n + 1];
+    le |= (uint32_t)(xe & 15) << (4 * n);
+    lo |= (uint32_t)(xo & 15) << (4 * n);
+    he |= (uint32_t)((xe >> 4) & 15) << (4 * n);
+    ho |= (uint32_t)((xo >> 4) & 15) << (4 * n);
+  }
+  uint4 nib = make_uint4(le, lo, he, ho);
+  *(uint4*)(act_row + act_nib_off(K) + 16 * (size_t)g) = nib;
+  uint32_t pm[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    pm[k] = (uint32_t)(q[k] & 255) | ((uint32_t)(q[4 + k] & 255) << 8) |
+            ((uint32_t)(q[8 + k] & 255) << 16) | ((uint32_t)(q[12 + k] & 255) << 24);
+  }
+  *(uint4*)(act_row + act_perm_off(K) + 16 * (size_t)g) = make_uint4(pm[0], pm[1], pm[2], pm[3]);
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Quantizer: one 256-thread block per token
+// ---------------------------------------------------------------------------
+constexpr int QT = 256;
+constexpr int QTILE = 4096;  // elements per pass of the sequential chains
+
+__global__ __launch_bounds__(QT) void k_quantize(const float* __restrict__ x, int n, int x_stride,
+                                                 const float* __restrict__ gamma,
+                                                 float* __restrict__ x_norm,
+                                                 int8_t* __restrict__ xq, int quant_stride,
+                                                 float* __restrict__ scale_out,
+                                                 float* __restrict__ max_out,
+                                                 uint8_t* __restrict__ act, size_t act_stride) {
+  __shared__ __attribute__((aligned(16))) float sq[4][QTILE / 4 + 4];
+  __shared__ float s_chain[4];
+  __shared__ float s_rms;
+  __shared__ float s_wmax[QT / 64];
+
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const float* __restrict__ xr = x + (size_t)m * x_stride;
+  const int n4 = n & ~3;
+
+  // (1) four sequential chains over x[4i+j]^2, one lane each
+  float chain = 0.0f;
+  for (int t0 = 0; t0 < n4; t0 += QTILE) {
+    const int cnt = min(QTILE, n4 - t0);
+    for (int i = tid; i < cnt; i += QT) {
+      const float v = xr[t0 + i];
+      sq[i & 3][i >> 2] = __fmul_rn(v, v);
+    }
+    __syncthreads();
+    if (tid < 4) {
+      const float* c = sq[tid];
+      const int len = cnt >> 2;
+      int i = 0;
+      for (; i + 8 <= len; i += 8) {
+        const float4 a = *(const float4*)(c + i);
+        const float4 b = *(const float4*)(c + i + 4);
+        chain = __fadd_rn(chain, a.x);
+        chain = __fadd_rn(chain, a.y);
+        chain = __fadd_rn(chain, a.z);
+        chain = __fadd_rn(chain, a.w);
+        chain = __fadd_rn(chain, b.x);
+        chain = __fadd_rn(chain, b.y);
+        chain = __fadd_rn(chain, b.z);
+        chain = __fadd_rn(chain, b.w);
+      }
+      for (; i < len; ++i) chain = __fadd_rn(chain, c[i]);
+    }
+    __syncthreads();
+  }
+  if (tid < 4) s_chain[tid] = chain;
+  __syncthreads();
+  if (tid == 0) {
+    float sum = __fadd_rn(__fadd_rn(__fadd_rn(s_chain[0], s_chain[1]), s_chain[2]), s_chain[3]);
+    for (int i = n4; i < n; ++i) sum = __fadd_rn(sum, __fmul_rn(xr[i], xr[i]));
+    s_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)n), 1e-6f)));
+  }
+  __syncthreads();
+  const float rms = s_rms;
+
+  // (2) max |(x*rms)*w| over the row (exact in any order)
+  float mx = 0.0f;
+  for (int i = tid; i < n; i += QT) {
+    const float v = __fmul_rn(__fmul_rn(xr[i], rms), gamma[i]);
+    mx = fmaxf(mx, fabsf(v));
+  }
+  mx = wave_max_f32(mx);
+  if (lane == 0) s_wmax[wave] = mx;
+  __syncthreads();
+  float max_abs = s_wmax[0];
+#pragma unroll
+  for (int w = 1; w < QT / 64; ++w) max_abs = fmaxf(max_abs, s_wmax[w]);
+
+  const float scale_x = __fdiv_rn(127.0f, __fadd_rn(max_abs, 1e-5f));
+  if (tid == 0) {
+    if (scale_out) scale_out[m] = scale_x;
+    if (max_out) max_out[m] = max_abs;
+  }
+
+  // (3) normalized values, int8, activation workspace; thread = 16 columns
+  uint8_t* __restrict__ arow = act ? act + (size_t)m * act_stride : nullptr;
+  const int n_groups = (n + 15) >> 4;
+  for (int g0 = 0; g0 < n_groups; g0 += QT) {
+    const int g = g0 + tid;
+    int q[16];
+    int qsum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int c = 16 * g + j;
+      int iv = 0;
+      if (c < n) {
+        const float v = __fmul_rn(__fmul_rn(xr[c], rms), gamma[c]);
+        if (x_norm) x_norm[(size_t)m * n + c] = v;
+        const float t = __fmul_rn(v, scale_x);
+        const float r = __fadd_rn(t, t >= 0.0f ? 0.5f : -0.5f);
+        iv = (int)r;
+        iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+        if (xq) xq[(size_t)m * quant_stride + c] = (int8_t)iv;
+      }
+      q[j] = iv;
+      qsum += iv;
+    }
+    if (arow) {
+      if (g < n_groups) write_act_group(arow, n, g, q);
+      // 64 groups = one 1024-column slice = one wave of this pass
+      const int s = wave_sum_i32(g < n_groups ? qsum : 0);
+      const int slice = (g0 >> 6) + wave;
+      if (lane == 0 && slice < slices_of(n)) ((int*)arow)[slice] = s;
+    }
+  }
+}
+
+// int8 activations given directly (stress shape): workspace only
+__global__ __launch_bounds__(QT) void k_prep_i8(const int8_t* __restrict__ xq, int ldx, int K,
+                                                uint8_t* __restrict__ act, size_t act_stride) {
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int8_t* __restrict__ xr = xq + (size_t)m * ldx;
+  uint8_t* __restrict__ arow = act + (size_t)m * act_stride;
+  const int n_groups = (K + 15) >> 4;
+  for (int g0 = 0; g0 < n_groups; g0 += QT) {
+    const int g = g0 + tid;
+    int q[16];
+    int qsum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int c = 16 * g + j;
+      q[j] = c < K ? (int)xr[c] : 0;
+      qsum += q[j];
+    }
+    if (g < n_groups) write_act_group(arow, K, g, q);
+    const int s = wave_sum_i32(g < n_groups ? qsum : 0);
+    const int slice = (g0 >> 6) + wave;
+    if (lane == 0 && slice < slices_of(K)) ((int*)arow)[slice] = s;
+  }
+}
+
+__device__ __forceinline__ float inv_scale_of(float scale_x, float w_scale) {
+  return __fdiv_rn(1.0f, __fmul_rn(scale_x, w_scale));  // src/kernel.c:391
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV (v_dot8 on split nibbles).  K % 64 == 0, K <= 64*64*P.
+//   T lanes per row (16/32/64), each lane owns 64 columns (16 packed bytes)
+//   per pass; P passes cover K.  16 consecutive lanes = one 1024-column
+//   slice, reduced with xor shuffles inside the 16-lane group.
+// ---------------------------------------------------------------------------
+template <int T, int P, int UNR, bool CANON, bool I32>
+__global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, size_t act_stride,
+                                              const float* __restrict__ scale_x,
+                                              const uint8_t* __restrict__ W, int N, int K,
+                                              float w_scale, float* __restrict__ out,
+                                              int32_t* __restrict__ out_i32) {
+  constexpr int RPW = 64 / T;  // rows per wave per row-group
+  const int m = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int u = lane % T, sub = lane / T, unit_base = sub * T;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n_waves = gridDim.x * 4;
+  const int chunks = K >> 6;
+  const size_t wstride = (size_t)(K >> 2);
+
+  const uint8_t* __restrict__ arow = act + (size_t)m * act_stride;
+  const int* __restrict__ ssum = (const int*)arow;
+  const uint4* __restrict__ anib = (const uint4*)(arow + act_nib_off(K));
+
+  // activations of this lane's chunks: 4 groups x {le, lo, he, ho}
+  uint32_t xa[P][16];
+  int xs[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int j = p * T + u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint4 v = j < chunks ? anib[4 * j + g] : make_uint4(0, 0, 0, 0);
+      xa[p][4 * g + 0] = v.x;
+      xa[p][4 * g + 1] = v.y;
+      xa[p][4 * g + 2] = v.z;
+      xa[p][4 * g + 3] = v.w;
+    }
+    xs[p] = ssum[(p * T + u) / 16 < slices_of(K) ? (p * T + u) / 16 : 0];
+  }
+  const float inv = I32 ? 0.0f : inv_scale_of(scale_x[m], w_scale);
+
+  const int n_rg = (N + RPW - 1) / RPW;
+  for (int base = gw; base < n_rg; base += n_waves * UNR) {
+    uint4 wv[UNR][P];
+    int rows[UNR];
+#pragma unroll
+    for (int i = 0; i < UNR; ++i) {
+      const int rg = base + i * n_waves;
+      rows[i] = rg * RPW + sub;
+      const bool ok = rg < n_rg && rows[i] < N;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int j = p * T + u;
+        wv[i][p] = (ok && j < chunks)
+                       ? *(const uint4*)(W + (size_t)rows[i] * wstride + 16 * (size_t)j)
+                       : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < UNR; ++i) {
+      float o = 0.0f;
+      int tot = 0;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const uint32_t w4[4] = {wv[i][p].x, wv[i][p].y, wv[i][p].z, wv[i][p].w};
+        uint32_t al = 0;
+        int ah = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t pw = CANON ? w4[d] : canon_codes(w4[d]);
+          const uint32_t lo = pw & 0x33333333u;
+          const uint32_t hi = (pw >> 2) & 0x33333333u;
+          al = __builtin_amdgcn_udot8(lo, xa[p][4 * d + 0], al, false);
+          al = __builtin_amdgcn_udot8(hi, xa[p][4 * d + 1], al, false);
+          ah = __builtin_amdgcn_sdot8((int)lo, (int)xa[p][4 * d + 2], ah, false);
+          ah = __builtin_amdgcn_sdot8((int)hi, (int)xa[p][4 * d + 3], ah, false);
+        }
+        int part = ah * 16 + (int)al;
+        part += __shfl_xor(part, 8, 64);
+        part += __shfl_xor(part, 4, 64);
+        part += __shfl_xor(part, 2, 64);
+        part += __shfl_xor(part, 1, 64);
+        const int t = part - xs[p];  // exact slice total of x.w
+        if (I32) {
+#pragma unroll
+          for (int q = 0; q < T / 16; ++q) tot += __shfl(t, unit_base + 16 * q, 64);
+        } else {
+          const float f = __fmul_rn((float)t, inv);
+#pragma unroll
+          for (int q = 0; q < T / 16; ++q) {
+            const float fq = __shfl(f, unit_base + 16 * q, 64);
+            // slices past K contribute nothing (they do not exist there)
+            if (p * (T / 16) + q < slices_of(K)) o = __fadd_rn(o, fq);
+          }
+        }
+      }
+      const int rg = base + i * n_waves;
+      if (u == 0 && rg < n_rg && rows[i] < N) {
+        if (I32)
+          out_i32[(size_t)m * N + rows[i]] = tot;
+        else
+          out[(size_t)m * N + rows[i]] = o;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic product for any K (K % 64 != 0 or very long rows): one wave per
+// row, plain int8 activations, 1024-column slices then the K % 4 remainder.
+// ---------------------------------------------------------------------------
+template <bool I32>
+__global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, int ldx,
+                                                 const float* __restrict__ scale_x,
+                                                 const uint8_t* __restrict__ W, int N, int K,
+                                                 float w_scale, float* __restrict__ out,
+                                                 int32_t* __restrict__ out_i32) {
+  const int m = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= N) return;  // whole wave leaves together
+  const int8_t* __restrict__ xr = xq + (size_t)m * ldx;
+  const uint8_t* __restrict__ row = W + (size_t)r * ((K + 3) / 4);
+  const int n_groups = K / 4;
+  const float inv = I32 ? 0.0f : inv_scale_of(scale_x[m], w_scale);
+  float o = 0.0f;
+  int tot = 0;
+  for (int g0 = 0; g0 < n_groups; g0 += 256) {
+    const int g1 = min(g0 + 256, n_groups);
+    int part = 0;
+    for (int g = g0 + lane; g < g1; g += 64) {
+      const uint32_t b = row[g];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int w = (int)((b >> (2 * j)) & 3u) - 1;
+        w = w > 1 ? 1 : w;
+        part += w * (int)xr[4 * g + j];
+      }
+    }
+    part = wave_sum_i32(part);
+    if (I32)
+      tot += part;
+    else
+      o = __fadd_rn(o, __fmul_rn((float)part, inv));
+  }
+  if (4 * n_groups < K) {
+    int rem = 0;
+    const uint32_t b = row[n_groups];
+    for (int c = 4 * n_groups; c < K; ++c) {
+      int w = (int)((b >> (2 * (c & 3))) & 3u) - 1;
+      w = w > 1 ? 1 : w;
+      rem += w * (int)xr[c];
+    }
+    if (I32)
+      tot += rem;
+    else
+      o = __fadd_rn(o, __fmul_rn((float)rem, inv));
+  }
+  if (lane == 0) {
+    if (I32)
+      out_i32[(size_t)m * N + r] = tot;
+    else
+      out[(size_t)m * N + r] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill / batched GEMM on int8 MFMA (v_mfma_i32_32x32x32_i8).
+//   block 256 threads = 2x2 waves, tile 128(M) x 128(N), K step 128.
+//   A (permuted int8 activations) staged in LDS; B decoded from the packed
+//   bytes straight into MFMA operand registers: a 16-byte load gives a lane
+//   64 columns of one weight row, i.e. its operand for four 32-deep steps.
+//   Lane (j = lane%32, h = lane/32) covers columns kb + 64h + 16s.. in step
+//   s, for A and B alike.  int32 accumulators are folded into fp32 at every
+//   1024-column slice boundary in slice order.
+// ---------------------------------------------------------------------------
+constexpr int GBM = 128, GBN = 128, GBK = 128, GLDA = GBK + 16;
+
+template <bool CANON, bool I32>
+__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ act, size_t act_stride,
+                                              const float* __restrict__ scale_x, int M,
+                                              const uint8_t* __restrict__ W, int N, int K,
+                                              float w_scale, float* __restrict__ out,
+                                              int32_t* __restrict__ out_i32) {
+  __shared__ __attribute__((aligned(16))) int8_t sA[GBM * GLDA];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int j32 = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
+  const size_t wstride = (size_t)(K >> 2);
+  const size_t perm = act_perm_off(K);
+
+  v16i acc[2][2];
+  float o[2][2][16];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc[a][b][v] = 0;
+        o[a][b][v] = 0.0f;
+      }
+    }
+
+  // rows of the accumulator elements this lane owns (C layout of 32x32)
+  // row = 8*(v/4) + 4*h + v%4 within the 32-row tile
+  for (int kb = 0; kb < K; kb += GBK) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int idx = tid + q * 256;
+      const int row = idx >> 3, c16 = idx & 7;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (m0 + row < M)
+        v = *(const uint4*)(act + (size_t)(m0 + row) * act_stride + perm + kb + 16 * c16);
+      *(uint4*)(sA + row * GLDA + 16 * c16) = v;
+    }
+    __syncthreads();
+
+    v4i bop[2][4];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int n = n0 + wn * 64 + nt * 32 + j32;
+      uint4 wv = make_uint4(0, 0, 0, 0);
+      if (n < N) wv = *(const uint4*)(W + (size_t)n * wstride + (kb >> 2) + 16 * h);
+      const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t pw = CANON ? w4[s] : canon_codes(w4[s]);
+        bop[nt][s][0] = (int)(pw & 0x03030303u);
+        bop[nt][s][1] = (int)((pw >> 2) & 0x03030303u);
+        bop[nt][s][2] = (int)((pw >> 4) & 0x03030303u);
+        bop[nt][s][3] = (int)((pw >> 6) & 0x03030303u);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int i = wm * 64 + mt * 32 + j32;
+        const v4i aop = *(const v4i*)(sA + i * GLDA + 64 * h + 16 * s);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[nt][s], acc[mt][nt], 0, 0, 0);
+      }
+    }
+
+    const bool slice_end = ((kb + GBK) % kSlice == 0) || (kb + GBK >= K);
+    if (slice_end) {
+      const int slice = kb / kSlice;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          int sx = 0;
+          float inv = 0.0f;
+          if (r < M) {
+            sx = ((const int*)(act + (size_t)r * act_stride))[slice];
+            if (!I32) inv = inv_scale_of(scale_x[r], w_scale);
+          }
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            const int t = acc[mt][nt][v] - sx;
+            if (I32)
+              o[mt][nt][v] = __int_as_float(__float_as_int(o[mt][nt][v]) + t);
+            else
+              o[mt][nt][v] = __fadd_rn(o[mt][nt][v], __fmul_rn((float)t, inv));
+            acc[mt][nt][v] = 0;
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int n = n0 + wn * 64 + nt * 32 + j32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (r < M && n < N) {
+          if (I32)
+            out_i32[(size_t)r * N + n] = __float_as_int(o[mt][nt][v]);
+          else
+            out[(size_t)r * N + n] = o[mt][nt][v];
+        }
+      }
+    }
+}
+
+__global__ void k_canonicalize(uint32_t* __restrict__ p, size_t n_words) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n_words;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = canon_codes(p[i]);
+}
+
+__global__ void k_canonicalize_tail(uint8_t* __restrict__ p, size_t n) {
+  const size_t i = threadIdx.x;
+  if (i < n) p[i] = (uint8_t)canon_codes(p[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const float* gamma,
+                           float* x_norm, int8_t* xq, int quant_stride, float* scale_x,
+                           uint8_t* act, hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_quantize, dim3(M), dim3(QT), 0, s, x, n, x_stride, gamma, x_norm, xq,
+                     quant_stride, scale_x, (float*)nullptr, act, act_row_bytes(n));
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const float* x, int n, const float* gamma, float* out, float* max_out,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(k_quantize, dim3(1), dim3(QT), 0, s, x, n, n, gamma, out, (int8_t*)nullptr,
+                     0, (float*)nullptr, max_out, (uint8_t*)nullptr, (size_t)0);
+  return hipGetLastError();
+}
+
+hipError_t launch_prep_i8(const int8_t* xq, int M, int ldx, int K, uint8_t* act, hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_prep_i8, dim3(M), dim3(QT), 0, s, xq, ldx, K, act, act_row_bytes(K));
+  return hipGetLastError();
+}
+
+template <int T, int P, bool CANON, bool I32>
+static hipError_t gemv_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
+                         int K, float w_scale, float* out, int32_t* out_i32, hipStream_t s) {
+  constexpr int RPW = 64 / T;
+  const int n_rg = (N + RPW - 1) / RPW;
+  const int UNR = 2;
+  int waves = (n_rg + UNR - 1) / UNR;
+  int blocks = (waves + 3) / 4;
+  const int cap = 2048;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL((k_gemv<T, P, 2, CANON, I32>), dim3(blocks, M), dim3(256), 0, s, act,
+                     act_row_bytes(K), scale_x, W, N, K, w_scale, out, out_i32);
+  return hipGetLastError();
+}
+
+template <bool CANON, bool I32>
+static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
+                                int N, int K, float w_scale, float* out, int32_t* out_i32,
+                                hipStream_t s) {
+  if (K <= 1024) return gemv_t<16, 1, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
+  if (K <= 2048) return gemv_t<32, 1, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
+  if (K <= 4096) return gemv_t<64, 1, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
+  if (K <= 8192) return gemv_t<64, 2, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
+  return gemv_t<64, 4, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
+}
+
+template <bool CANON, bool I32>
+static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
+                         int K, float w_scale, float* out, int32_t* out_i32, hipStream_t s) {
+  dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
+  hipLaunchKernelGGL((k_gemm<CANON, I32>), grid, dim3(256), 0, s, act, act_row_bytes(K), scale_x,
+                     M, W, N, K, w_scale, out, out_i32);
+  return hipGetLastError();
+}
+
+// which kernel serves a product of this shape
+static int product_path(int M, int K) {
+  if (K % 64 != 0 || K > 16384) return 0;  // generic
+  if (M >= 32 && K % GBK == 0) return 2;   // MFMA GEMM
+  return 1;                                // GEMV per token
+}
+
+hipError_t launch_product(const uint8_t* act, const float* scale_x, int M, const uint8_t* packed,
+                          int N, int K, float w_scale, bool canonical, float* out,
+                          int32_t* out_i32, hipStream_t s) {
+  const bool i32 = out_i32 != nullptr;
+  switch (product_path(M, K)) {
+    case 2:
+      if (canonical)
+        return i32 ? gemm_t<true, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
+                   : gemm_t<true, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
+      return i32 ? gemm_t<false, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
+                 : gemm_t<false, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
+    case 1:
+      if (canonical)
+        return i32 ? gemv_dispatch<true, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
+                   : gemv_dispatch<true, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
+      return i32 ? gemv_dispatch<false, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
+                 : gemv_dispatch<false, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
+    default:
+      return hipErrorInvalidValue;  // caller uses launch_generic
+  }
+}
+
+bool product_needs_generic(int M, int K) { return product_path(M, K) == 0; }
+
+hipError_t launch_generic(const int8_t* xq, int ldx, const float* scale_x, int M,
+                          const uint8_t* packed, int N, int K, float w_scale, float* out,
+                          int32_t* out_i32, hipStream_t s) {
+  dim3 grid((N + 3) / 4, M);
+  if (out_i32)
+    hipLaunchKernelGGL(k_generic<true>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
+                       w_scale, out, out_i32);
+  else
+    hipLaunchKernelGGL(k_generic<false>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
+                       w_scale, out, out_i32);
+  return hipGetLastError();
+}
+
+hipError_t launch_canonicalize(uint8_t* p, size_t bytes, hipStream_t s) {
+  const size_t words = bytes / 4;
+  if (words) {
+    int blocks = (int)((words + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_canonicalize, dim3(blocks), dim3(256), 0, s, (uint32_t*)p, words);
+  }
+  if (bytes % 4)
+    hipLaunchKernelGGL(k_canonicalize_tail, dim3(1), dim3(64), 0, s, p + 4 * words, bytes % 4);
+  return hipGetLastError();
+}
+
+}  // namespace bm

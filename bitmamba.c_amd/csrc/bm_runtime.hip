@@ -1,0 +1,504 @@
+// Runtime of the BitLinear backend: lifecycle, weight registry, the
+// dispatch-table entry points (host pointers, synchronous) and the
+// device-pointer entry points.
+//
+// Threading: like the reference's Metal backend (src/metal/bm_metal.c:93-95)
+// every entry point serializes on one process-wide mutex; the reference calls
+// the dispatch-table kernels from its main thread only (src/block.c:362-370,
+// src/model.c:1225, 1259).
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "bm_common.h"
+#include "bm_hip.h"
+#include "bm_bit2.h"
+
+namespace bm {
+hipError_t launch_rms_norm(const float* x, int n, const float* gamma, float* out, float* max_out,
+                           hipStream_t s);
+bool product_needs_generic(int M, int K);
+hipError_t launch_generic(const int8_t* xq, int ldx, const float* scale_x, int M,
+                          const uint8_t* packed, int N, int K, float w_scale, float* out,
+                          int32_t* out_i32, hipStream_t s);
+}  // namespace bm
+
+static thread_local char g_err[512];
+
+extern "C" void bm_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+extern "C" const char* bm_hip_last_error(void) { return g_err; }
+
+namespace {
+
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+struct Registered {
+  void* dev = nullptr;
+  size_t bytes = 0;
+};
+
+struct Backend {
+  std::mutex mu;
+  bool ready = false;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // weights and float vectors by host address
+  std::unordered_map<const void*, Registered> packed;
+  std::unordered_map<const void*, Registered> floats;
+  // grow-on-demand device scratch for the host-pointer entry points
+  DevBuf d_x, d_out, d_norm, d_q, d_act, d_scale;
+  // pinned host staging
+  DevBuf h_stage;
+};
+
+Backend& B() {
+  static Backend* b = new Backend();  // intentionally leaked: no static dtor
+  return *b;
+}
+
+[[noreturn]] void die(const char* what) {
+  fprintf(stderr, "Fatal: HIP BitLinear backend: %s: %s\n", what, g_err);
+  exit(1);
+}
+
+bool ensure_dev(DevBuf& b, size_t bytes) {
+  if (b.bytes >= bytes && b.ptr) return true;
+  if (b.ptr) (void)hipFree(b.ptr);
+  b.ptr = nullptr;
+  b.bytes = 0;
+  size_t want = bytes < 4096 ? 4096 : bytes + bytes / 4;
+  BM_HIP_CHECK_RET(hipMalloc(&b.ptr, want), false);
+  b.bytes = want;
+  return true;
+}
+
+bool ensure_pinned(DevBuf& b, size_t bytes) {
+  if (b.bytes >= bytes && b.ptr) return true;
+  if (b.ptr) (void)hipHostFree(b.ptr);
+  b.ptr = nullptr;
+  b.bytes = 0;
+  size_t want = bytes < 65536 ? 65536 : bytes + bytes / 4;
+  BM_HIP_CHECK_RET(hipHostMalloc(&b.ptr, want, hipHostMallocDefault), false);
+  b.bytes = want;
+  return true;
+}
+
+bool init_locked(Backend& b) {
+  if (b.ready) return true;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    bm_set_error("no HIP device");
+    return false;
+  }
+  hipDeviceProp_t prop;
+  BM_HIP_CHECK_RET(hipGetDeviceProperties(&prop, 0), false);
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    bm_set_error("device 0 is %s, this build targets gfx950 only", prop.gcnArchName);
+    return false;
+  }
+  BM_HIP_CHECK_RET(hipSetDevice(0), false);
+  BM_HIP_CHECK_RET(hipStreamCreateWithFlags(&b.stream, hipStreamNonBlocking), false);
+  b.device = 0;
+  b.ready = true;
+  return true;
+}
+
+// Copies a packed tensor to an aligned device buffer and rewrites code 11.
+const uint8_t* register_packed(Backend& b, const uint8_t* host, size_t bytes) {
+  auto it = b.packed.find(host);
+  if (it != b.packed.end() && it->second.bytes >= bytes) return (const uint8_t*)it->second.dev;
+  if (it != b.packed.end()) {
+    (void)hipFree(it->second.dev);
+    b.packed.erase(it);
+  }
+  void* d = nullptr;
+  BM_HIP_CHECK_RET(hipMalloc(&d, bytes ? bytes : 1), nullptr);
+  BM_HIP_CHECK_RET(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, b.stream), nullptr);
+  BM_HIP_CHECK_RET(bm::launch_canonicalize((uint8_t*)d, bytes, b.stream), nullptr);
+  BM_HIP_CHECK_RET(hipStreamSynchronize(b.stream), nullptr);
+  b.packed[host] = Registered{d, bytes};
+  return (const uint8_t*)d;
+}
+
+const float* register_floats(Backend& b, const float* host, size_t count) {
+  const size_t bytes = count * sizeof(float);
+  auto it = b.floats.find(host);
+  if (it != b.floats.end() && it->second.bytes >= bytes) return (const float*)it->second.dev;
+  if (it != b.floats.end()) {
+    (void)hipFree(it->second.dev);
+    b.floats.erase(it);
+  }
+  void* d = nullptr;
+  BM_HIP_CHECK_RET(hipMalloc(&d, bytes ? bytes : 4), nullptr);
+  BM_HIP_CHECK_RET(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice), nullptr);
+  b.floats[host] = Registered{d, bytes};
+  return (const float*)d;
+}
+
+void bitlinear_check(int n, const struct tensor* w) {
+  // BITLINEAR_CHECK (src/bitmamba.h:219-231)
+  if (n != w->cols) {
+    fprintf(stderr, "Fatal: bitlinear dim mismatch n=%d vs cols=%d\n", n, w->cols);
+    exit(1);
+  }
+  if (!w->is_bitnet) {
+    fprintf(stderr, "Fatal: bitlinear requires packed BitNet weights\n");
+    exit(1);
+  }
+}
+
+// Host-pointer batch BitLinear: quantize + product on the device, results
+// copied back.  Any HIP failure is fatal (never zero outputs silently).
+void host_bitlinear(const float* x, int M, int n, const uint8_t* packed, int rows, int cols,
+                    float w_scale, const float* norm_w, float* out, float* x_norm_buf,
+                    int8_t* x_quant, int quant_stride) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (!init_locked(b)) die("init");
+  if (M <= 0) return;
+  const size_t wbytes = (size_t)rows * (size_t)((cols + 3) / 4);
+  const uint8_t* dW = register_packed(b, packed, wbytes);
+  const float* dG = register_floats(b, norm_w, (size_t)n);
+  if (!dW || !dG) die("weight upload");
+
+  const size_t xbytes = (size_t)M * n * sizeof(float);
+  const size_t obytes = (size_t)M * rows * sizeof(float);
+  const size_t qbytes = (size_t)M * n;
+  const size_t abytes = (size_t)M * bm::act_row_bytes(n);
+  if (!ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_out, obytes) ||
+      !ensure_dev(b.d_norm, xbytes) || !ensure_dev(b.d_q, qbytes) ||
+      !ensure_dev(b.d_act, abytes) || !ensure_dev(b.d_scale, (size_t)M * 4))
+    die("scratch allocation");
+  const size_t stage = xbytes > obytes + xbytes + qbytes ? xbytes : obytes + xbytes + qbytes;
+  if (!ensure_pinned(b.h_stage, stage)) die("pinned staging");
+
+  uint8_t* hs = (uint8_t*)b.h_stage.ptr;
+  memcpy(hs, x, xbytes);
+  hipStream_t s = b.stream;
+  hipError_t e = hipMemcpyAsync(b.d_x.ptr, hs, xbytes, hipMemcpyHostToDevice, s);
+  const bool generic = bm::product_needs_generic(M, cols);
+  if (e == hipSuccess)
+    e = bm::launch_quantize((const float*)b.d_x.ptr, M, n, n, dG, (float*)b.d_norm.ptr,
+                            (int8_t*)b.d_q.ptr, n, (float*)b.d_scale.ptr,
+                            generic ? nullptr : (uint8_t*)b.d_act.ptr, s);
+  if (e == hipSuccess) {
+    if (generic)
+      e = bm::launch_generic((const int8_t*)b.d_q.ptr, n, (const float*)b.d_scale.ptr, M, dW,
+                             rows, cols, w_scale, (float*)b.d_out.ptr, nullptr, s);
+    else
+      e = bm::launch_product((const uint8_t*)b.d_act.ptr, (const float*)b.d_scale.ptr, M, dW,
+                             rows, cols, w_scale, true, (float*)b.d_out.ptr, nullptr, s);
+  }
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(hs, b.d_out.ptr, obytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(hs + obytes, b.d_norm.ptr, xbytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(hs + obytes + xbytes, b.d_q.ptr, qbytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    bm_set_error("%s", hipGetErrorString(e));
+    die("bitlinear");
+  }
+  memcpy(out, hs, obytes);
+  // x_norm_buf is a single n-vector reused per token: the last token stays
+  if (x_norm_buf)
+    memcpy(x_norm_buf, hs + obytes + (size_t)(M - 1) * n * sizeof(float), (size_t)n * 4);
+  if (x_quant)
+    for (int m = 0; m < M; ++m)
+      memcpy(x_quant + (size_t)m * quant_stride, hs + obytes + xbytes + (size_t)m * n, (size_t)n);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Lifecycle
+// ---------------------------------------------------------------------------
+extern "C" bool bm_hip_init(void) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  return init_locked(b);
+}
+
+extern "C" bool bm_hip_available(void) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  return b.ready;
+}
+
+extern "C" bool bm_hip_set_mmap(const void* base, size_t size) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (!init_locked(b)) return false;
+  bm_bit2_view_t v;
+  if (bm_bit2_parse(base, size, &v) != 0) {
+    // not a BIT2 image: tensors are uploaded lazily on first use
+    return true;
+  }
+  for (int i = 0; i < v.n_tensors; ++i) {
+    const bm_bit2_tensor_t* t = &v.tensors[i];
+    if (t->is_bitnet) {
+      if (!register_packed(b, t->packed, (size_t)t->rows * (size_t)((t->cols + 3) / 4))) {
+        bm_bit2_view_free(&v);
+        return false;
+      }
+    } else if (!register_floats(b, t->data, t->n_elements)) {
+      bm_bit2_view_free(&v);
+      return false;
+    }
+  }
+  bm_bit2_view_free(&v);
+  return true;
+}
+
+extern "C" void bm_hip_cleanup(void) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (!b.ready) return;
+  (void)hipStreamSynchronize(b.stream);
+  for (auto& kv : b.packed) (void)hipFree(kv.second.dev);
+  for (auto& kv : b.floats) (void)hipFree(kv.second.dev);
+  b.packed.clear();
+  b.floats.clear();
+  for (DevBuf* d : {&b.d_x, &b.d_out, &b.d_norm, &b.d_q, &b.d_act, &b.d_scale}) {
+    if (d->ptr) (void)hipFree(d->ptr);
+    *d = DevBuf{};
+  }
+  if (b.h_stage.ptr) (void)hipHostFree(b.h_stage.ptr);
+  b.h_stage = DevBuf{};
+  (void)hipStreamDestroy(b.stream);
+  b.stream = nullptr;
+  b.ready = false;
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch-table entry points
+// ---------------------------------------------------------------------------
+extern "C" float hip_rms_norm(const float* x, int size, const float* weight, float* out) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (!init_locked(b)) die("init");
+  const float* dG = register_floats(b, weight, (size_t)size);
+  const size_t xbytes = (size_t)size * sizeof(float);
+  if (!dG || !ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_norm, xbytes) ||
+      !ensure_dev(b.d_scale, 16) || !ensure_pinned(b.h_stage, xbytes + 16))
+    die("rms_norm scratch");
+  uint8_t* hs = (uint8_t*)b.h_stage.ptr;
+  memcpy(hs, x, xbytes);
+  hipStream_t s = b.stream;
+  hipError_t e = hipMemcpyAsync(b.d_x.ptr, hs, xbytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = bm::launch_rms_norm((const float*)b.d_x.ptr, size, dG, (float*)b.d_norm.ptr,
+                            (float*)b.d_scale.ptr, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(hs, b.d_norm.ptr, xbytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(hs + xbytes, b.d_scale.ptr, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    bm_set_error("%s", hipGetErrorString(e));
+    die("rms_norm");
+  }
+  memcpy(out, hs, xbytes);
+  float mx;
+  memcpy(&mx, hs + xbytes, 4);
+  return mx;
+}
+
+extern "C" void hip_bitlinear_forward(const float* x, int n, const struct tensor* w,
+                                      const struct tensor* norm_w, float* out, float* x_norm_buf,
+                                      int8_t* x_quant_buf) {
+  bitlinear_check(n, w);
+  host_bitlinear(x, 1, n, w->packed_data, w->rows, w->cols, w->scale, norm_w->data, out,
+                 x_norm_buf, x_quant_buf, n);
+}
+
+extern "C" void hip_bitlinear_forward_batch(const float* x_batch, int n_tokens, int n,
+                                            const struct tensor* w, const struct tensor* norm_w,
+                                            float* out_batch, float* x_norm_buf,
+                                            int8_t* x_quant_batch, int quant_stride) {
+  bitlinear_check(n, w);
+  host_bitlinear(x_batch, n_tokens, n, w->packed_data, w->rows, w->cols, w->scale, norm_w->data,
+                 out_batch, x_norm_buf, x_quant_batch, quant_stride);
+}
+
+extern "C" void bm_hip_bitlinear_forward_batch(const float* x_batch, int n_tokens, int n,
+                                               const uint8_t* packed_data, int rows, int cols,
+                                               float w_scale, const float* norm_weight,
+                                               float* out_batch, float* x_norm_buf,
+                                               int8_t* x_quant_batch, int quant_stride) {
+  if (n != cols) {
+    fprintf(stderr, "Fatal: bitlinear dim mismatch n=%d vs cols=%d\n", n, cols);
+    exit(1);
+  }
+  host_bitlinear(x_batch, n_tokens, n, packed_data, rows, cols, w_scale, norm_weight, out_batch,
+                 x_norm_buf, x_quant_batch, quant_stride);
+}
+
+extern "C" bool bm_hip_register(bm_hip_dispatch_t* t) {
+  if (!t || !bm_hip_init()) return false;
+  t->rms_norm = (void*)&hip_rms_norm;
+  t->bitlinear_forward = (void*)&hip_bitlinear_forward;
+  t->bitlinear_forward_batch = (void*)&hip_bitlinear_forward_batch;
+  t->bitlinear_prepare = nullptr;
+  t->bitlinear_row_worker = nullptr;
+  t->name = "hip";
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Device memory helpers
+// ---------------------------------------------------------------------------
+extern "C" void* bm_hip_malloc(size_t bytes) {
+  if (!bm_hip_init()) return nullptr;
+  void* p = nullptr;
+  BM_HIP_CHECK_RET(hipMalloc(&p, bytes ? bytes : 1), nullptr);
+  return p;
+}
+
+extern "C" void bm_hip_free(void* dev) {
+  if (dev) (void)hipFree(dev);
+}
+
+extern "C" int bm_hip_memcpy_h2d(void* dev, const void* host, size_t bytes) {
+  BM_HIP_CHECK_RET(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice), -1);
+  return 0;
+}
+
+extern "C" int bm_hip_memcpy_d2h(void* host, const void* dev, size_t bytes) {
+  BM_HIP_CHECK_RET(hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost), -1);
+  return 0;
+}
+
+extern "C" int bm_hip_memset(void* dev, int value, size_t bytes) {
+  BM_HIP_CHECK_RET(hipMemset(dev, value, bytes), -1);
+  return 0;
+}
+
+extern "C" int bm_hip_synchronize(void) {
+  BM_HIP_CHECK_RET(hipDeviceSynchronize(), -1);
+  return 0;
+}
+
+static hipStream_t stream_or_default(void* s) {
+  return s ? (hipStream_t)s : B().stream;
+}
+
+extern "C" int bm_hip_canonicalize_dev(uint8_t* packed, size_t bytes, void* stream) {
+  if (!bm_hip_init()) return -1;
+  BM_HIP_CHECK_RET(bm::launch_canonicalize(packed, bytes, stream_or_default(stream)), -1);
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Device-pointer kernels
+// ---------------------------------------------------------------------------
+extern "C" size_t bm_hip_act_bytes(int M, int n) {
+  if (M <= 0 || n <= 0) return 0;
+  return (size_t)M * bm::act_row_bytes(n);
+}
+
+extern "C" size_t bm_hip_i8_act_bytes(int M, int K) { return bm_hip_act_bytes(M, K); }
+
+extern "C" int bm_hip_quantize_dev(const float* x, int M, int n, int x_stride,
+                                   const float* norm_w, float* x_norm, int8_t* x_quant,
+                                   int quant_stride, float* scale_x, void* act, void* stream) {
+  if (!bm_hip_init()) return -1;
+  if (M < 0 || n <= 0 || x_stride < n || !x || !norm_w || !scale_x ||
+      (x_quant && quant_stride < n)) {
+    bm_set_error("quantize: invalid arguments (M=%d n=%d x_stride=%d)", M, n, x_stride);
+    return -2;
+  }
+  if (act && n % 16 != 0) {
+    bm_set_error("quantize: activation workspace needs n %% 16 == 0 (n=%d)", n);
+    return -2;
+  }
+  BM_HIP_CHECK_RET(bm::launch_quantize(x, M, n, x_stride, norm_w, x_norm, x_quant, quant_stride,
+                                       scale_x, (uint8_t*)act, stream_or_default(stream)),
+                   -1);
+  return 0;
+}
+
+extern "C" int bm_hip_bitlinear_act_dev(const void* act, const float* scale_x, int M,
+                                        const uint8_t* packed, int N, int K, float w_scale,
+                                        int canonical, float* out, void* stream) {
+  if (!bm_hip_init()) return -1;
+  if (M < 0 || N <= 0 || K <= 0 || !act || !scale_x || !packed || !out) {
+    bm_set_error("bitlinear_act: invalid arguments");
+    return -2;
+  }
+  if (bm::product_needs_generic(M, K)) {
+    bm_set_error("bitlinear_act: K=%d needs the int8 path (bm_hip_bitlinear_dev)", K);
+    return -2;
+  }
+  BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, scale_x, M, packed, N, K, w_scale,
+                                      canonical != 0, out, nullptr, stream_or_default(stream)),
+                   -1);
+  return 0;
+}
+
+extern "C" int bm_hip_bitlinear_dev(const float* x, int M, int K, const float* norm_w,
+                                    const uint8_t* packed, int N, float w_scale, int canonical,
+                                    float* out, int8_t* x_quant, int quant_stride, float* scale_x,
+                                    void* act, void* stream) {
+  if (!bm_hip_init()) return -1;
+  if (M < 0 || N <= 0 || K <= 0 || !x || !norm_w || !packed || !out || !x_quant || !scale_x ||
+      quant_stride < K) {
+    bm_set_error("bitlinear: invalid arguments");
+    return -2;
+  }
+  hipStream_t s = stream_or_default(stream);
+  const bool generic = bm::product_needs_generic(M, K);
+  if (!generic && !act) {
+    bm_set_error("bitlinear: act workspace required");
+    return -2;
+  }
+  BM_HIP_CHECK_RET(bm::launch_quantize(x, M, K, K, norm_w, nullptr, x_quant, quant_stride, scale_x,
+                                       generic ? nullptr : (uint8_t*)act, s),
+                   -1);
+  if (generic)
+    BM_HIP_CHECK_RET(bm::launch_generic(x_quant, quant_stride, scale_x, M, packed, N, K, w_scale,
+                                        out, nullptr, s),
+                     -1);
+  else
+    BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, scale_x, M, packed, N, K, w_scale,
+                                        canonical != 0, out, nullptr, s),
+                     -1);
+  return 0;
+}
+
+extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
+                                           const uint8_t* packed, int N, int K, int canonical,
+                                           int32_t* out, void* act, void* stream) {
+  if (!bm_hip_init()) return -1;
+  if (M < 0 || N <= 0 || K <= 0 || ldx < K || !xq || !packed || !out) {
+    bm_set_error("ternary_gemm_i32: invalid arguments");
+    return -2;
+  }
+  hipStream_t s = stream_or_default(stream);
+  if (bm::product_needs_generic(M, K)) {
+    BM_HIP_CHECK_RET(bm::launch_generic(xq, ldx, nullptr, M, packed, N, K, 0.0f, nullptr, out, s),
+                     -1);
+    return 0;
+  }
+  if (!act) {
+    bm_set_error("ternary_gemm_i32: act workspace required");
+    return -2;
+  }
+  BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act, s), -1);
+  BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, nullptr, M, packed, N, K, 0.0f,
+                                      canonical != 0, nullptr, out, s),
+                   -1);
+  return 0;
+}

@@ -1,0 +1,261 @@
+/*
+ * bm_hip.h -- C ABI of the MI355X (gfx950) BitLinear backend.
+ *
+ * Drop-in for the ternary BitLinear hot path of jserv/bitmamba.c.  The
+ * backend takes the slot the Metal backend fills in the reference
+ * (src/metal/bm_metal.h:14-99) and registers its kernels in the reference's
+ * plugin table kernel_dispatch_t g_kernels (src/dispatch.h:86-100).
+ *
+ * Every entry point takes plain pointers and sizes.  Functions whose names
+ * start with hip_ have exactly the function-pointer types of the dispatch
+ * table and take HOST pointers (synchronous, like the CPU kernels they
+ * replace).  Functions ending in _dev take DEVICE pointers and a HIP stream
+ * (void *, NULL = the library's stream) and are asynchronous.
+ *
+ * Errors: contract violations (dimension mismatch, non-BitNet weights) exit
+ * the process like BITLINEAR_CHECK (src/bitmamba.h:219-231); a HIP runtime
+ * failure inside a hip_ kernel entry point also prints and exits -- outputs
+ * are never silently zeroed (contrast src/metal/bm_metal.c:549-553).
+ * Lifecycle and _dev functions return false / a negative code instead, with
+ * the reason in bm_hip_last_error().
+ */
+#pragma once
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The reference's tensor view (src/bitmamba.h:65-74).  The layout below is
+ * the one the reference compiles; define BM_HIP_HAVE_TENSOR_T when the
+ * reference's own bitmamba.h is already included. */
+#ifndef BM_HIP_HAVE_TENSOR_T
+struct tensor {
+    const float *data;          /* float32 weights */
+    const uint8_t *packed_data; /* packed 2-bit weights, [rows][ceil(cols/4)] */
+    int rows;
+    int cols;
+    size_t n_elements;
+    bool is_bitnet;
+    float scale;
+};
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Lifecycle -- mirrors src/metal/bm_metal.h:14-24, 44-45               */
+/* ------------------------------------------------------------------ */
+
+/* bm_metal_init (src/metal/bm_metal.h:15): selects device 0, creates the
+ * library stream.  false if no gfx950 device is usable. */
+bool bm_hip_init(void);
+/* bm_metal_available (src/metal/bm_metal.h:18) */
+bool bm_hip_available(void);
+/* bm_metal_set_mmap (src/metal/bm_metal.h:24): registers a model image.
+ * When the image parses as BIT2 (src/model.c:477-932 layout) every packed
+ * tensor is copied once into its own 256-byte-aligned device buffer with
+ * the 2-bit code 11 rewritten to 10 (same value, src/quantization.c:27-31),
+ * and every float tensor is copied too; hip_* calls then find them by host
+ * pointer.  Host tensors that were never registered are uploaded on first
+ * use.  Registered host memory must not change afterwards. */
+bool bm_hip_set_mmap(const void *base, size_t size);
+/* bm_metal_cleanup (src/metal/bm_metal.h:45) */
+void bm_hip_cleanup(void);
+/* Reason for the last false / negative return. */
+const char *bm_hip_last_error(void);
+
+/* ------------------------------------------------------------------ */
+/* Dispatch-table kernels (host pointers, synchronous)                  */
+/* ------------------------------------------------------------------ */
+
+/* rms_norm_fn_t (src/dispatch.h:20-23); semantics of scalar_rms_norm
+ * (src/kernel.c:72-129), bit-exact. */
+float hip_rms_norm(const float *x, int size, const float *weight, float *out);
+
+/* bitlinear_forward_fn_t (src/dispatch.h:25-31); semantics of
+ * scalar_bitlinear_forward (src/kernel.c:346-448), bit-exact fp32 output.
+ * x_norm_buf[n] and x_quant_buf[n] receive what the scalar kernel leaves
+ * there. */
+void hip_bitlinear_forward(const float *x,
+                           int n,
+                           const struct tensor *w,
+                           const struct tensor *norm_w,
+                           float *out,
+                           float *x_norm_buf,
+                           int8_t *x_quant_buf);
+
+/* bitlinear_forward_batch_fn_t (src/dispatch.h:33-42); semantics of
+ * scalar_bitlinear_forward_batch (src/kernel.c:322-338).  x_norm_buf holds
+ * the last token's normalized input afterwards, as in the reference. */
+void hip_bitlinear_forward_batch(const float *x_batch,
+                                 int n_tokens,
+                                 int n,
+                                 const struct tensor *w,
+                                 const struct tensor *norm_w,
+                                 float *out_batch,
+                                 float *x_norm_buf,
+                                 int8_t *x_quant_batch,
+                                 int quant_stride);
+
+/* Layout mirror of kernel_dispatch_t (src/dispatch.h:87-95). */
+typedef struct {
+    void *rms_norm;
+    void *bitlinear_forward;
+    void *bitlinear_forward_batch;
+    void *bitlinear_prepare;
+    void *bitlinear_row_worker;
+    void *ssm_inner;
+    const char *name;
+} bm_hip_dispatch_t;
+
+/* The GPU branch of dispatch_init (src/dispatch.c:15-52): sets rms_norm,
+ * bitlinear_forward and bitlinear_forward_batch to the hip_ entries,
+ * bitlinear_prepare and bitlinear_row_worker to NULL (so block_step takes
+ * its unfused path, src/block.c:280, 361-371, and the LM head calls
+ * bitlinear_forward, src/model.c:1258-1262), keeps ssm_inner, and sets
+ * name = "hip".  Returns false (table untouched) if the backend is not
+ * available. */
+bool bm_hip_register(bm_hip_dispatch_t *table);
+
+/* bm_metal_bitlinear_forward_batch (src/metal/bm_metal.h:31-42): the same
+ * computation as hip_bitlinear_forward_batch from raw tensor fields. */
+void bm_hip_bitlinear_forward_batch(const float *x_batch,
+                                    int n_tokens,
+                                    int n,
+                                    const uint8_t *packed_data,
+                                    int rows,
+                                    int cols,
+                                    float w_scale,
+                                    const float *norm_weight,
+                                    float *out_batch,
+                                    float *x_norm_buf,
+                                    int8_t *x_quant_batch,
+                                    int quant_stride);
+
+/* ------------------------------------------------------------------ */
+/* Device memory helpers (for callers without a HIP runtime of their    */
+/* own; no counterpart in the reference)                                */
+/* ------------------------------------------------------------------ */
+void *bm_hip_malloc(size_t bytes);
+void bm_hip_free(void *dev);
+int bm_hip_memcpy_h2d(void *dev, const void *host, size_t bytes);
+int bm_hip_memcpy_d2h(void *host, const void *dev, size_t bytes);
+int bm_hip_memset(void *dev, int value, size_t bytes);
+int bm_hip_synchronize(void);
+/* Rewrites 2-bit code 11 to 10 in place (device buffer of `bytes`). */
+int bm_hip_canonicalize_dev(uint8_t *packed, size_t bytes, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Device-pointer kernels (asynchronous on `stream`)                    */
+/* ------------------------------------------------------------------ */
+
+/* Per-token RMSNorm + absmax int8 quantization, bit-exact with
+ * src/kernel.c:72-129 + 356-386, for M tokens of n values (row stride
+ * x_stride floats).  Writes x_quant[m*quant_stride + i] and scale_x[m];
+ * x_norm (nullable) gets [m*n + i].  Also fills the activation workspace
+ * `act` (bm_hip_act_bytes(M, n) bytes) used by the _dev products below. */
+size_t bm_hip_act_bytes(int M, int n);
+int bm_hip_quantize_dev(const float *x,
+                        int M,
+                        int n,
+                        int x_stride,
+                        const float *norm_w,
+                        float *x_norm,
+                        int8_t *x_quant,
+                        int quant_stride,
+                        float *scale_x,
+                        void *act,
+                        void *stream);
+
+/* Ternary BitLinear product on quantized activations (the act workspace
+ * from bm_hip_quantize_dev): out[m*N + r] (fp32) with the scalar kernel's
+ * 1024-column block epilogue (src/kernel.c:255-256, 407-447), bit-exact.
+ * `canonical` != 0 promises the packed bytes hold no code 11. */
+int bm_hip_bitlinear_act_dev(const void *act,
+                             const float *scale_x,
+                             int M,
+                             const uint8_t *packed,
+                             int N,
+                             int K,
+                             float w_scale,
+                             int canonical,
+                             float *out,
+                             void *stream);
+
+/* Quantize + product in one call (device pointers): scalar_bitlinear_
+ * forward_batch semantics for M tokens. `act` as above. */
+int bm_hip_bitlinear_dev(const float *x,
+                         int M,
+                         int K,
+                         const float *norm_w,
+                         const uint8_t *packed,
+                         int N,
+                         float w_scale,
+                         int canonical,
+                         float *out,
+                         int8_t *x_quant,
+                         int quant_stride,
+                         float *scale_x,
+                         void *act,
+                         void *stream);
+
+/* Exact int32 product of int8 activations and ternary weights:
+ * out[m*N + r] = sum_k xq[m*ldx + k] * decode(W[r][k]) (stress shape;
+ * activations need no quantization).  M = 1 runs the decode GEMV, larger M
+ * the int8 MFMA GEMM.  Needs bm_hip_i8_act_bytes(M, K) bytes of `act`. */
+size_t bm_hip_i8_act_bytes(int M, int K);
+int bm_hip_ternary_gemm_i32_dev(const int8_t *xq,
+                                int M,
+                                int ldx,
+                                const uint8_t *packed,
+                                int N,
+                                int K,
+                                int canonical,
+                                int32_t *out,
+                                void *act,
+                                void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Synthetic BIT2 images (counterpart: the writer scripts/export-bin.py  */
+/* :99-199; no libm, bit-reproducible on any host)                      */
+/* ------------------------------------------------------------------ */
+enum {
+    BM_SYNTH_UNIFORM = 0,   /* p(-1)=p(0)=p(+1)=1/3 */
+    BM_SYNTH_P0_40 = 1,     /* p(0)=0.4, p(+-1)=0.3 */
+    BM_SYNTH_P0_60 = 2,     /* p(0)=0.6, p(+-1)=0.2 */
+    BM_SYNTH_RAW_BYTES = 3, /* all four 2-bit codes, 11 included */
+};
+
+typedef struct {
+    int vocab;
+    int d_model;
+    int n_layers;
+    int n_heads;
+    int in_proj_rows; /* 0: 2*d_inner + 3*n_heads (src/model.c:683-701) */
+    int ternary_dist; /* BM_SYNTH_* */
+    float fp_sigma;   /* std of every float tensor */
+    float ternary_scale;
+    uint64_t seed;
+} bm_synth_config_t;
+
+size_t bm_bit2_synth_size(const bm_synth_config_t *c);
+int bm_bit2_synth_write(const bm_synth_config_t *c, void *dst, size_t len);
+void bm_synth_ternary(uint64_t seed,
+                      int tensor,
+                      int rows,
+                      int cols,
+                      int dist,
+                      uint8_t *packed);
+void bm_synth_normal(uint64_t seed,
+                     int tensor,
+                     size_t n,
+                     float sigma,
+                     float *out);
+void bm_synth_int8(uint64_t seed, int tensor, size_t n, int8_t *out);
+void bm_synth_prompt(uint64_t seed, int vocab, int n, int32_t *tokens);
+
+#ifdef __cplusplus
+}
+#endif

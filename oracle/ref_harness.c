@@ -1,0 +1,238 @@
+/*
+ * Harness around the reference's own C sources (compiled where they lie by
+ * oracle/Makefile into oracle/_ref/libbmref.so).  Test infrastructure only:
+ * it is used to pin the oracle restatement and as the timed CPU baseline.
+ *
+ * It exposes flat entry points (plain pointers and sizes) over the
+ * reference's kernel dispatch table and model API:
+ *   - dispatch selection: dispatch_init() (src/dispatch.c:15-52), optionally
+ *     overwritten with the scalar kernels and a NULL bitlinear_prepare so that
+ *     block_step takes its unfused path (src/block.c:280, 361-371);
+ *   - bitlinear / rms_norm / ssm_inner through g_kernels
+ *     (src/dispatch.h:86-97);
+ *   - model_load / model_prefill / model_forward_step / model_free
+ *     (src/bitmamba.h:282-294) for end-to-end greedy streams.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "bitmamba.h"
+#include "dispatch.h"
+#include "threadpool.h"
+
+static int32_t *g_lut_buf;
+
+/* kind: 0 = scalar (the oracle semantics), 1 = whatever dispatch_init picks
+ * on this CPU (AVX2+FMA on x86-64). */
+const char *bmref_init(int threads, int kind)
+{
+    bm_set_threads(threads);
+    bm_set_poll(0);
+    dispatch_init();
+    init_lut();
+    if (kind == 0) {
+        g_kernels.rms_norm = scalar_rms_norm;
+        g_kernels.bitlinear_forward = scalar_bitlinear_forward;
+        g_kernels.bitlinear_forward_batch = scalar_bitlinear_forward_batch;
+        g_kernels.bitlinear_prepare = NULL;
+        g_kernels.bitlinear_row_worker = NULL;
+        g_kernels.ssm_inner = scalar_ssm_inner;
+        g_kernels.name = "scalar";
+    }
+    if (!g_lut_buf)
+        g_lut_buf = xmalloc_aligned(256 * 16 * sizeof(int32_t), 64);
+    scalar_set_lut_buf(g_lut_buf);
+    return g_kernels.name;
+}
+
+void bmref_shutdown(void)
+{
+    bm_thread_pool_free();
+}
+
+int bmref_threads(void)
+{
+    return bm_get_threads();
+}
+
+static void make_weight(tensor_t *w,
+                        const uint8_t *packed,
+                        int rows,
+                        int cols,
+                        float scale)
+{
+    memset(w, 0, sizeof(*w));
+    w->packed_data = packed;
+    w->rows = rows;
+    w->cols = cols;
+    w->n_elements = (size_t) rows * cols;
+    w->is_bitnet = true;
+    w->scale = scale;
+}
+
+static void make_vec(tensor_t *t, const float *data, int n)
+{
+    memset(t, 0, sizeof(*t));
+    t->data = data;
+    t->rows = n;
+    t->n_elements = (size_t) n;
+    t->scale = 1.0f;
+}
+
+float bmref_rms_norm(const float *x, int n, const float *w, float *out)
+{
+    return g_kernels.rms_norm(x, n, w, out);
+}
+
+void bmref_bitlinear_forward(const float *x,
+                             int n,
+                             const uint8_t *packed,
+                             int rows,
+                             int cols,
+                             float scale,
+                             const float *norm_w,
+                             float *out,
+                             float *x_norm_buf,
+                             int8_t *x_quant_buf)
+{
+    tensor_t w, nw;
+    make_weight(&w, packed, rows, cols, scale);
+    make_vec(&nw, norm_w, n);
+    g_kernels.bitlinear_forward(x, n, &w, &nw, out, x_norm_buf, x_quant_buf);
+}
+
+void bmref_bitlinear_forward_batch(const float *x,
+                                   int n_tokens,
+                                   int n,
+                                   const uint8_t *packed,
+                                   int rows,
+                                   int cols,
+                                   float scale,
+                                   const float *norm_w,
+                                   float *out,
+                                   float *x_norm_buf,
+                                   int8_t *x_quant,
+                                   int quant_stride)
+{
+    tensor_t w, nw;
+    make_weight(&w, packed, rows, cols, scale);
+    make_vec(&nw, norm_w, n);
+    g_kernels.bitlinear_forward_batch(x, n_tokens, n, &w, &nw, out, x_norm_buf,
+                                      x_quant, quant_stride);
+}
+
+/* Row kernel alone on a given int8 vector (no quantization): the AVX2
+ * decomposed worker when available, used for the int8-input stress shape. */
+int bmref_row_worker_available(void)
+{
+    return g_kernels.bitlinear_row_worker != NULL;
+}
+
+void bmref_rows_int8(const int8_t *x_quant,
+                     const uint8_t *packed,
+                     int rows,
+                     int cols,
+                     float inv_scale,
+                     float *out)
+{
+    bitlinear_row_work_t work = {
+        .x_quant = x_quant,
+        .packed_data = packed,
+        .out = out,
+        .inv_scale = inv_scale,
+        .rows = rows,
+        .cols = cols,
+        .packed_stride = (cols + 3) / 4,
+        .chunk_ctr = NULL,
+        .chunk_size = 0,
+    };
+    bm_parallel_for(rows, g_kernels.bitlinear_row_worker, &work);
+}
+
+void bmref_ssm_inner(const ssm_inner_args_t *a, int idx_start, int idx_end)
+{
+    g_kernels.ssm_inner(a, idx_start, idx_end);
+}
+
+void bmref_rng_seed(uint64_t s)
+{
+    rng_seed(s);
+}
+
+uint64_t bmref_rng_next(void)
+{
+    return rng_next();
+}
+
+void bmref_lut(int8_t *unpack /* [256*4] */,
+               uint8_t *pmask /* [256] */,
+               uint8_t *nmask /* [256] */)
+{
+    init_lut();
+    memcpy(unpack, UNPACK_LUT, sizeof(UNPACK_LUT));
+    memcpy(pmask, TMAC_P_MASK, sizeof(TMAC_P_MASK));
+    memcpy(nmask, TMAC_N_MASK, sizeof(TMAC_N_MASK));
+}
+
+/* ---- model API ---- */
+
+void *bmref_model_load(const char *path)
+{
+    bitmamba_model_t *m = calloc(1, sizeof(*m));
+    if (!m)
+        return NULL;
+    m->use_gpu = false;
+    if (!model_load(m, path)) {
+        free(m);
+        return NULL;
+    }
+    return m;
+}
+
+void bmref_model_free(void *h)
+{
+    if (!h)
+        return;
+    model_free((bitmamba_model_t *) h);
+    free(h);
+}
+
+void bmref_model_prefill(void *h, const int32_t *tokens, int n)
+{
+    model_prefill((bitmamba_model_t *) h, tokens, n);
+}
+
+int bmref_model_step(void *h,
+                     int token,
+                     const int *history,
+                     int history_len,
+                     float penalty)
+{
+    return model_forward_step((bitmamba_model_t *) h, token, history,
+                              history_len, penalty, 0.0f, 0.0f, 1.0f, 0);
+}
+
+const float *bmref_model_logits(void *h)
+{
+    return ((bitmamba_model_t *) h)->logits;
+}
+
+int bmref_model_vocab(void *h)
+{
+    return ((bitmamba_model_t *) h)->config.vocab_size;
+}
+
+/* Copy of one layer's recurrent state: conv_state [(d_conv-1)*d_inner],
+ * ssm_state [d_inner], conv_pos. */
+int bmref_model_layer_state(void *h,
+                            int layer,
+                            float *conv_state,
+                            float *ssm_state)
+{
+    bitmamba_model_t *m = (bitmamba_model_t *) h;
+    bitmamba_block_t *b = &m->layers[layer];
+    memcpy(conv_state, b->conv_state,
+           (size_t) (b->d_conv - 1) * b->d_inner * sizeof(float));
+    memcpy(ssm_state, b->ssm_state, (size_t) b->d_inner * sizeof(float));
+    return b->conv_pos;
+}

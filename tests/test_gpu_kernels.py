@@ -1,0 +1,264 @@
+"""GPU parity of the gfx950 kernels against the oracle and the golden
+fixtures, through the C ABI.
+
+Bar: int8, int32 and fp32 outputs bit-exact (the fp32 epilogue follows the
+scalar kernel's 1024-column block order, so no tolerance is needed; the
+north-star tolerance 1e-4 relative is asserted as a second, looser line in
+the fp32 tests so a failure shows how far off it is).
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import native
+from native import bh, ptr
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+DB = bh.DeviceBuffer
+
+
+def rnd(seed):
+    return np.random.default_rng(seed)
+
+
+def note(msg):
+    print("[case] " + msg, flush=True)
+
+
+def rel_err(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+# ------------------------------------------------------------ helpers
+def gpu_quantize(hip, x, g, act=True):
+    M, n = x.shape
+    dx, dg = DB.from_array(x), DB.from_array(g)
+    dn, dq, ds = DB(x.nbytes), DB(M * n), DB(4 * M)
+    da = DB(bh.lib().bm_hip_act_bytes(M, n)) if act else None
+    bh.check(hip.bm_hip_quantize_dev(dx.ptr, M, n, n, dg.ptr, dn.ptr, dq.ptr, n, ds.ptr,
+                                     da.ptr if da else None, None), "quantize")
+    hip.bm_hip_synchronize()
+    return (dn.download((M, n), np.float32), dq.download((M, n), np.int8),
+            ds.download(M, np.float32))
+
+
+def gpu_bitlinear(hip, x, packed, N, K, scale, g, canonical=0):
+    M = x.shape[0]
+    dx, dg, dw = DB.from_array(x), DB.from_array(g), DB.from_array(packed)
+    do, dq, ds = DB(4 * M * N), DB(M * K), DB(4 * M)
+    da = DB(hip.bm_hip_act_bytes(M, K))
+    bh.check(hip.bm_hip_bitlinear_dev(dx.ptr, M, K, dg.ptr, dw.ptr, N, scale, canonical, do.ptr,
+                                      dq.ptr, K, ds.ptr, da.ptr, None), "bitlinear_dev")
+    hip.bm_hip_synchronize()
+    return do.download((M, N), np.float32), dq.download((M, K), np.int8)
+
+
+def gpu_gemm_i32(hip, xq, packed, N, K, canonical=0):
+    M = xq.shape[0]
+    dx, dw = DB.from_array(xq), DB.from_array(packed)
+    do, da = DB(4 * M * N), DB(hip.bm_hip_i8_act_bytes(M, K))
+    bh.check(hip.bm_hip_ternary_gemm_i32_dev(dx.ptr, M, K, dw.ptr, N, K, canonical, do.ptr,
+                                             da.ptr, None), "gemm_i32")
+    hip.bm_hip_synchronize()
+    return do.download((M, N), np.int32)
+
+
+# ------------------------------------------------------------ quantizer
+def test_quantize_golden(hip):
+    z = np.load(os.path.join(GOLD, "quant_vectors.npz"))
+    for n in (1024, 4096, 4099, 100):
+        note("quantize golden n=%d" % n)
+        x, g = z["x_%d" % n], z["g_%d" % n]
+        xn, xq, _ = gpu_quantize(hip, x, g, act=(n % 16 == 0))
+        assert xn.tobytes() == z["xn_%d" % n].tobytes()
+        np.testing.assert_array_equal(xq, z["xq_%d" % n])
+
+
+@pytest.mark.parametrize("n", [1024, 2048, 4096, 8192, 1040])
+def test_quantize_random_vs_oracle(hip, n):
+    note("quantize random n=%d" % n)
+    r = rnd(n)
+    M = 96
+    scales = 10.0 ** r.uniform(-4, 4, (M, 1))
+    x = (r.standard_normal((M, n)) * scales).astype(np.float32)
+    x[::7, r.integers(0, n, 5)] *= 100.0
+    g = (r.standard_normal(n) * 0.02).astype(np.float32)
+    xn, xq, sc = gpu_quantize(hip, x, g)
+    on, oq, osc, _ = native.orc_quantize_rows(x, g)
+    assert xn.tobytes() == on.tobytes()
+    np.testing.assert_array_equal(xq, oq)
+    assert sc.tobytes() == osc.tobytes()
+
+
+def test_rms_norm_dropin(hip):
+    r = rnd(3)
+    for n in (1024, 2048, 777):
+        note("hip_rms_norm n=%d" % n)
+        x = r.standard_normal(n).astype(np.float32)
+        g = r.standard_normal(n).astype(np.float32)
+        out = np.empty(n, np.float32)
+        mx = hip.hip_rms_norm(ptr(x), n, ptr(g), ptr(out))
+        ref = np.empty(n, np.float32)
+        rmx = native.oracle().orc_rms_norm(ptr(x), n, ptr(g), ptr(ref))
+        assert out.tobytes() == ref.tobytes()
+        assert np.float32(mx) == np.float32(rmx)
+
+
+# ------------------------------------------------------------ int32 products
+GEMV_SHAPES = [(1024, 4384), (2048, 8512), (4096, 2048), (8192, 1000), (1024, 50257),
+               (512, 100), (1536, 77), (2560, 33), (16384, 40)]
+
+
+@pytest.mark.parametrize("K,N", GEMV_SHAPES)
+@pytest.mark.parametrize("canonical", [0, 1])
+def test_gemv_i32_exact(hip, K, N, canonical):
+    note("gemv i32 K=%d N=%d canonical=%d" % (K, N, canonical))
+    r = rnd(K + N + canonical)
+    if canonical:
+        packed = bh.synth_ternary(K, N, N, K, bh.SYNTH_UNIFORM)
+    else:
+        packed = r.integers(0, 256, (N, K // 4), dtype=np.uint8)
+    xq = r.integers(-128, 128, (1, K), dtype=np.int8)
+    got = gpu_gemm_i32(hip, xq, packed, N, K, canonical)
+    np.testing.assert_array_equal(got, native.orc_gemm_i32(xq, packed, N, K))
+
+
+@pytest.mark.parametrize("M,K,N", [(32, 1024, 128), (100, 2048, 200), (256, 1024, 333),
+                                   (64, 4096, 64), (40, 8192, 129), (16, 8192, 512),
+                                   (3, 1024, 50)])
+def test_gemm_i32_exact(hip, M, K, N):
+    note("gemm i32 M=%d K=%d N=%d" % (M, K, N))
+    r = rnd(M * 3 + K + N)
+    packed = r.integers(0, 256, (N, K // 4), dtype=np.uint8)
+    xq = r.integers(-128, 128, (M, K), dtype=np.int8)
+    got = gpu_gemm_i32(hip, xq, packed, N, K)
+    np.testing.assert_array_equal(got, native.orc_gemm_i32(xq, packed, N, K))
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_stress_exact_small_m(hip, M):
+    """Stress shape K = N = 8192, p(0)=0.6, int8 activations, full check."""
+    K = N = 8192
+    note("stress M=%d" % M)
+    packed = bh.synth_ternary(5, 1, N, K, bh.SYNTH_P0_60)
+    xq = bh.synth_int8(5, 2, (M, K))
+    got = gpu_gemm_i32(hip, xq, packed, N, K, canonical=1)
+    np.testing.assert_array_equal(got, native.orc_gemm_i32(xq, packed, N, K))
+
+
+def test_stress_m4096_sampled_and_linear(hip):
+    """M=4096 at full size: 4096 sampled entries checked exactly, plus
+    linearity in the activations (size-independent)."""
+    K = N = 8192
+    M = 4096
+    note("stress M=4096")
+    packed = bh.synth_ternary(5, 1, N, K, bh.SYNTH_P0_60)
+    xq = bh.synth_int8(5, 3, (M, K))
+    got = gpu_gemm_i32(hip, xq, packed, N, K, canonical=1)
+    r = rnd(9)
+    ms = r.integers(0, M, 64)
+    ns = r.integers(0, N, 64)
+    w = native.decode_dense(packed[ns], K).astype(np.int64)
+    expect = xq[ms].astype(np.int64) @ w.T
+    np.testing.assert_array_equal(got[np.ix_(ms, ns)], expect)
+    # every row of the last tile and a full column
+    np.testing.assert_array_equal(got[M - 1], native.orc_gemm_i32(xq[M - 1:], packed, N, K)[0])
+    # linearity: (a + b) with |a|,|b| <= 63 stays in int8
+    a = (xq[:256] // 2).astype(np.int8)
+    b = (xq[:256] - a).astype(np.int8)
+    ga = gpu_gemm_i32(hip, a, packed, N, K, 1)
+    gb = gpu_gemm_i32(hip, b, packed, N, K, 1)
+    np.testing.assert_array_equal(ga + gb, got[:256])
+
+
+# ------------------------------------------------------------ fp32 BitLinear
+FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257),
+             (3, 1024, 300), (1, 1000, 77), (2, 1026, 33), (1, 100, 10),
+             (48, 2048, 520), (40, 4096, 260)]
+
+
+@pytest.mark.parametrize("M,K,N", FP_SHAPES)
+def test_bitlinear_fp32_exact(hip, M, K, N):
+    note("bitlinear fp32 M=%d K=%d N=%d" % (M, K, N))
+    r = rnd(M + K * 3 + N)
+    packed = r.integers(0, 256, (N, (K + 3) // 4), dtype=np.uint8)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    x[:, r.integers(0, K, 3)] *= 10.0
+    g = (r.standard_normal(K) * 0.02).astype(np.float32)
+    out, xq = gpu_bitlinear(hip, x, packed, N, K, 0.02, g)
+    ref, _, rq = native.orc_bitlinear(x, packed, N, K, 0.02, g)
+    np.testing.assert_array_equal(xq, rq)
+    assert rel_err(out, ref) <= 1e-4
+    assert out.tobytes() == ref.tobytes()
+
+
+def test_prefill_shapes_sampled(hip):
+    """Prefill GEMM shapes M=2048: K=2048->N=8512 and K=4096->N=2048, fp32,
+    activations N(0,1) with 1% outliers x10; 40 token rows (first/last tile
+    included) checked bit-exactly against the oracle."""
+    r = rnd(2048)
+    for K, N, seed in ((2048, 8512, 11), (4096, 2048, 12)):
+        note("prefill M=2048 K=%d N=%d" % (K, N))
+        M = 2048
+        packed = bh.synth_ternary(seed, 1, N, K, bh.SYNTH_UNIFORM)
+        x = bh.synth_normal(seed, 2, (M, K), 1.0)
+        mask = r.random((M, K)) < 0.01
+        x[mask] *= 10.0
+        g = np.ones(K, np.float32)
+        out, xq = gpu_bitlinear(hip, x, packed, N, K, 0.02, g, canonical=1)
+        rows = np.unique(np.concatenate([[0, 1, 127, 128, M - 1], r.integers(0, M, 35)]))
+        ref, _, rq = native.orc_bitlinear(x[rows], packed, N, K, 0.02, g)
+        np.testing.assert_array_equal(xq[rows], rq)
+        assert out[rows].tobytes() == ref.tobytes()
+
+
+# ------------------------------------------------------------ drop-in ABI
+def test_dropin_cfg1_golden(hip):
+    from golden.make_golden import cfg1_inputs, sha, CFG1
+    z = np.load(os.path.join(GOLD, "bitlinear_k1024_n4384.npz"))
+    packed, x, g = cfg1_inputs()
+    assert sha(packed) == str(z["packed_sha256"]) and sha(x) == str(z["x_sha256"])
+    K, N = CFG1["K"], CFG1["N"]
+    w = bh.make_tensor(packed, N, K, CFG1["scale"])
+    nw = bh.make_tensor(data=g)
+    out = np.empty(N, np.float32)
+    xn = np.empty(K, np.float32)
+    xq = np.zeros(K + 32, np.int8)
+    hip.hip_bitlinear_forward(ptr(x), K, C.byref(w), C.byref(nw), ptr(out), ptr(xn), ptr(xq))
+    assert out.tobytes() == z["out"][0].tobytes()
+    assert xn.tobytes() == z["x_norm"].tobytes()
+    np.testing.assert_array_equal(xq[:K], z["x_quant"][0])
+
+
+def test_dropin_batch_golden_shapes(hip):
+    z = np.load(os.path.join(GOLD, "bitlinear_shapes.npz"))
+    for key in sorted(k[4:] for k in z.files if k.startswith("out_")):
+        K, N = map(int, key.split("_"))
+        note("drop-in batch golden K=%d N=%d" % (K, N))
+        p, x, g = z["packed_" + key], z["x_" + key], z["g_" + key]
+        M = x.shape[0]
+        w = bh.make_tensor(p, N, K, 0.037)
+        nw = bh.make_tensor(data=g)
+        out = np.empty((M, N), np.float32)
+        xn = np.empty(K, np.float32)
+        xq = np.zeros((M, K + 32), np.int8)
+        hip.hip_bitlinear_forward_batch(ptr(x), M, K, C.byref(w), C.byref(nw), ptr(out),
+                                        ptr(xn), ptr(xq), K + 32)
+        assert out.tobytes() == z["out_" + key].tobytes()
+        np.testing.assert_array_equal(xq[:, :K], z["xq_" + key])
+
+
+def test_register_table(hip):
+    t = bh.Dispatch()
+    t.ssm_inner = 1234
+    assert hip.bm_hip_register(C.byref(t))
+    assert t.name == b"hip" and t.bitlinear_prepare is None and t.bitlinear_row_worker is None
+    assert t.ssm_inner == 1234 and t.bitlinear_forward and t.rms_norm
+
+
+def test_set_mmap_registers_model(hip):
+    blob = bh.synth_model(1000, 128, 2, 4, 5, bh.SYNTH_RAW_BYTES)
+    assert hip.bm_hip_set_mmap(ptr(blob), blob.nbytes)

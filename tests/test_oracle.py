@@ -1,0 +1,272 @@
+"""The oracle (oracle/bm_oracle.c) pinned three ways:
+
+* against the reference's own C compiled here (oracle/_ref, scalar kernels
+  forced): bit-exact for every fp32 and int8 output;
+* against closed forms in numpy (decode table, int32 brute force);
+* against invariants the scalar path must satisfy (scale invariance of the
+  int8 vector, the largest element quantizing to +-127, ties away from zero).
+"""
+import numpy as np
+import pytest
+
+import native
+from native import bh, ptr
+
+
+def rnd(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- a1 decode
+def test_decode_closed_form():
+    O = native.oracle()
+    assert [O.orc_decode_weight(b) for b in range(4)] == [-1, 0, 1, 1]
+    unpack = np.empty((256, 4), np.int8)
+    pm = np.empty(256, np.uint8)
+    nm = np.empty(256, np.uint8)
+    O.orc_luts(ptr(unpack), ptr(pm), ptr(nm))
+    b = np.arange(256, dtype=np.uint8)[:, None]
+    expect = native.decode_dense(b, 4)
+    np.testing.assert_array_equal(unpack, expect)
+    np.testing.assert_array_equal(pm, ((expect == 1) * (1 << np.arange(4))).sum(1))
+    np.testing.assert_array_equal(nm, ((expect == -1) * (1 << np.arange(4))).sum(1))
+
+
+def test_decode_vs_reference(ref_lib):
+    O = native.oracle()
+    ref_lib.bmref_init(1, 0)
+    tabs = [np.empty((256, 4), np.int8), np.empty(256, np.uint8), np.empty(256, np.uint8)]
+    rtabs = [np.empty_like(t) for t in tabs]
+    O.orc_luts(*(ptr(t) for t in tabs))
+    ref_lib.bmref_lut(*(ptr(t) for t in rtabs))
+    for a, b in zip(tabs, rtabs):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_prng_vs_reference(ref_lib):
+    import ctypes as C
+    O = native.oracle()
+    for seed in (1, 42, 0xDEADBEEF):
+        ref_lib.bmref_rng_seed(seed)
+        st = C.c_uint64(seed)
+        for _ in range(100):
+            assert O.orc_rng_next(C.byref(st)) == ref_lib.bmref_rng_next()
+
+
+# ------------------------------------------------------- a3/a4 rms + quant
+@pytest.mark.parametrize("n", [1, 3, 4, 7, 64, 1000, 1024, 2048, 4096, 4099])
+def test_rms_norm_vs_reference(ref_lib, n):
+    ref_lib.bmref_init(1, 0)
+    O = native.oracle()
+    r = rnd(n)
+    for trial in range(5):
+        x = (r.standard_normal(n) * (10.0 ** r.integers(-3, 3))).astype(np.float32)
+        g = r.standard_normal(n).astype(np.float32)
+        a = np.empty(n, np.float32)
+        b = np.empty(n, np.float32)
+        ma = O.orc_rms_norm(ptr(x), n, ptr(g), ptr(a))
+        mb = ref_lib.bmref_rms_norm(ptr(x), n, ptr(g), ptr(b))
+        assert np.float32(ma).tobytes() == np.float32(mb).tobytes()
+        assert a.tobytes() == b.tobytes()
+
+
+def test_quantize_invariants():
+    r = rnd(7)
+    n = 2048
+    g = np.ones(n, np.float32)
+    x = r.standard_normal((20, n)).astype(np.float32)
+    xn, xq, sc, mx = native.orc_quantize_rows(x, g)
+    # the element of largest magnitude maps to +-127 (v*scale just under 127)
+    for m in range(20):
+        i = np.argmax(np.abs(xn[m]))
+        assert abs(int(xq[m, i])) == 127
+    assert np.all(np.abs(xq.astype(int)) <= 127)
+    # RMSNorm makes the int8 vector invariant to a power-of-two input scale
+    _, xq2, _, _ = native.orc_quantize_rows(x * np.float32(8.0), g)
+    np.testing.assert_array_equal(xq, xq2)
+    # ties go away from zero: v = k + 0.5 exactly
+    O = native.oracle()
+    v = np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -0.49], np.float32)
+    q = np.empty(v.size, np.int8)
+    # max_abs chosen so that scale_x == 1.0f exactly: 127/(126+1e-5) != 1,
+    # so quantize with max such that 127/(max+1e-5f) rounds to 1.0f
+    mx = np.float32(127.0) - np.float32(1e-5)
+    sc = O.orc_quantize(ptr(v), v.size, float(mx), ptr(q))
+    assert sc == 1.0
+    assert q.tolist() == [1, -1, 2, -2, 3, -3, 127, 0]
+
+
+# ------------------------------------------------- a5-a8 bitlinear forward
+SHAPES = [(1024, 64), (1024, 4384), (2048, 257), (4096, 96), (1000, 33), (1026, 17),
+          (64, 5), (3, 4), (8192, 40)]
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_bitlinear_vs_reference(ref_lib, K, N):
+    ref_lib.bmref_init(1, 0)
+    r = rnd(K * 131 + N)
+    packed = r.integers(0, 256, (N, (K + 3) // 4), dtype=np.uint8)  # codes 11 included
+    M = 3
+    x = r.standard_normal((M, K)).astype(np.float32)
+    x[1] *= 50
+    g = (r.standard_normal(K) * 0.5).astype(np.float32)
+    a = native.orc_bitlinear(x, packed, N, K, 0.02, g)
+    b = native.ref_bitlinear(x, packed, N, K, 0.02, g)
+    for u, v in zip(a, b):
+        assert u.tobytes() == v.tobytes()
+
+
+@pytest.mark.parametrize("K,N", [(1024, 50), (2048, 31), (1030, 9), (4096, 12)])
+def test_slice_totals_closed_form(K, N):
+    r = rnd(K + N)
+    packed = r.integers(0, 256, (N, (K + 3) // 4), dtype=np.uint8)
+    xq = r.integers(-128, 128, K, dtype=np.int8)
+    st, rt = native.orc_slice_totals(xq, packed, N, K)
+    w = native.decode_dense(packed, K).astype(np.int64)
+    x = xq.astype(np.int64)
+    ng = K // 4
+    for s in range(st.shape[1]):
+        c0, c1 = 1024 * s, min(1024 * (s + 1), 4 * ng)
+        np.testing.assert_array_equal(st[:, s], w[:, c0:c1] @ x[c0:c1])
+    np.testing.assert_array_equal(rt, w[:, 4 * ng:] @ x[4 * ng:])
+    full = native.orc_gemm_i32(xq[None, :], packed, N, K)[0]
+    np.testing.assert_array_equal(full, w @ x)
+
+
+def test_rows_epilogue_order():
+    """fp32 out = sum over 1024-blocks of fl(total*inv) in block order: a
+    dropped or reordered block changes the low bits."""
+    r = rnd(3)
+    K, N = 4096, 64
+    packed = r.integers(0, 256, (N, K // 4), dtype=np.uint8)
+    xq = r.integers(-128, 128, K, dtype=np.int8)
+    inv = np.float32(0.0123457)
+    out = np.empty(N, np.float32)
+    native.oracle().orc_tmac_rows_f32(ptr(xq), ptr(packed), N, K, float(inv), ptr(out))
+    st, _ = native.orc_slice_totals(xq, packed, N, K)
+    acc = np.zeros(N, np.float32)
+    for s in range(4):
+        acc = (acc + (st[:, s].astype(np.float32) * inv).astype(np.float32)).astype(np.float32)
+    assert out.tobytes() == acc.tobytes()
+
+
+# ----------------------------------------------------------- a15 SSM step
+def test_ssm_inner_vs_reference(ref_lib):
+    import ctypes as C
+    ref_lib.bmref_init(1, 0)
+
+    class Args(C.Structure):
+        _fields_ = [(n, C.c_void_p) for n in
+                    ("z", "x", "B", "C", "dt", "dt_bias", "A", "cw", "cb", "cs0", "cs1", "cs2",
+                     "csw", "state", "D", "y")] + [("head_dim", C.c_int), ("d_inner", C.c_int),
+                                                   ("n_heads", C.c_int)]
+
+    ref_lib.bmref_ssm_inner.argtypes = [C.POINTER(Args), C.c_int, C.c_int]
+    r = rnd(11)
+    di, nh = 512, 8
+    proj = (r.standard_normal(2 * di + 3 * nh) * 3).astype(np.float32)
+    dtb = r.standard_normal(nh).astype(np.float32)
+    A = -np.exp(r.standard_normal(nh)).astype(np.float32)
+    cw = r.standard_normal((4, di)).astype(np.float32)
+    cb = r.standard_normal(di).astype(np.float32)
+    D = r.standard_normal(di).astype(np.float32)
+    cs = r.standard_normal((3, di)).astype(np.float32)
+    st = r.standard_normal(di).astype(np.float32)
+    proj[2 * di + 2 * nh] = 30.0  # softplus linear branch
+
+    outs = []
+    for who in ("orc", "ref"):
+        cs_ = cs.copy()
+        st_ = st.copy()
+        y = np.empty(di, np.float32)
+        p_ = proj.copy()
+        if who == "orc":
+            native.oracle().orc_ssm_inner(ptr(p_), di, nh, ptr(dtb), ptr(A), ptr(cw), ptr(cb),
+                                          ptr(cs_[0]), ptr(cs_[1]), ptr(cs_[2]), ptr(st_),
+                                          ptr(D), ptr(y), 0, di)
+        else:
+            base = p_.ctypes.data
+            a = Args(base, base + 4 * di, base + 8 * di, base + 8 * di + 4 * nh,
+                     base + 8 * di + 8 * nh, dtb.ctypes.data, A.ctypes.data, cw.ctypes.data,
+                     cb.ctypes.data, cs_[0].ctypes.data, cs_[1].ctypes.data, cs_[2].ctypes.data,
+                     cs_[0].ctypes.data, st_.ctypes.data, D.ctypes.data, y.ctypes.data,
+                     di // nh, di, nh)
+            ref_lib.bmref_ssm_inner(C.byref(a), 0, di)
+        outs.append((cs_, st_, y))
+    for u, v in zip(*outs):
+        assert u.tobytes() == v.tobytes()
+
+
+# --------------------------------------------------- end-to-end (model)
+def _tiny_model(seed, dist=bh.SYNTH_UNIFORM, vocab=1000, d_model=128, n_layers=2, n_heads=4):
+    return bh.synth_model(vocab, d_model, n_layers, n_heads, seed, dist)
+
+
+def _ref_stream(ref_lib, path, prompt, steps):
+    h = ref_lib.bmref_model_load(path.encode())
+    assert h
+    try:
+        if len(prompt) > 1:
+            p = np.ascontiguousarray(prompt[:-1], np.int32)
+            ref_lib.bmref_model_prefill(h, ptr(p), len(p))
+        hist = list(prompt)
+        cur = int(prompt[-1])
+        toks, logits = [], []
+        V = ref_lib.bmref_model_vocab(h)
+        for _ in range(steps):
+            harr = np.array(hist[-256:], np.int32)
+            cur = ref_lib.bmref_model_step(h, cur, ptr(harr), len(harr), 1.0)
+            toks.append(cur)
+            logits.append(np.ctypeslib.as_array(ref_lib.bmref_model_logits(h), (V,)).copy())
+            hist.append(cur)
+        return toks, logits
+    finally:
+        ref_lib.bmref_model_free(h)
+
+
+def orc_stream(blob, prompt, steps):
+    O = native.oracle()
+    h = O.orc_model_load(ptr(blob), blob.nbytes)
+    assert h
+    try:
+        if len(prompt) > 1:
+            p = np.ascontiguousarray(prompt[:-1], np.int32)
+            O.orc_model_prefill(h, ptr(p), len(p))
+        hist = list(prompt)
+        cur = int(prompt[-1])
+        V = O.orc_model_config(h, 0)
+        toks, logits = [], []
+        for _ in range(steps):
+            harr = np.array(hist[-256:], np.int32)
+            cur = O.orc_model_step(h, cur, ptr(harr), len(harr), 1.0)
+            toks.append(cur)
+            logits.append(np.ctypeslib.as_array(O.orc_model_logits(h), (V,)).copy())
+            hist.append(cur)
+        return toks, logits
+    finally:
+        O.orc_model_free(h)
+
+
+@pytest.mark.parametrize("seed,dist", [(5, bh.SYNTH_UNIFORM), (6, bh.SYNTH_P0_40)])
+def test_model_vs_reference(ref_lib, tmp_path, seed, dist):
+    ref_lib.bmref_init(2, 0)
+    blob = _tiny_model(seed, dist)
+    path = tmp_path / "m.bin"
+    blob.tofile(path)
+    prompt = bh.synth_prompt(seed, 1000, 8)
+    t1, l1 = orc_stream(blob, prompt, 12)
+    t2, l2 = _ref_stream(ref_lib, str(path), prompt, 12)
+    assert t1 == t2
+    for a, b in zip(l1, l2):
+        assert a.tobytes() == b.tobytes()
+
+
+def test_model_loader_rejects_malformed():
+    O = native.oracle()
+    blob = _tiny_model(1)
+    assert O.orc_model_load(ptr(blob), blob.nbytes)  # sanity (leaks a handle: tiny)
+    bad = blob.copy()
+    bad[:4] = 0
+    assert not O.orc_model_load(ptr(bad), bad.nbytes)
+    trunc = blob[: blob.nbytes // 2].copy()
+    assert not O.orc_model_load(ptr(trunc), trunc.nbytes)
