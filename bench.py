@@ -1,0 +1,257 @@
+"""Benchmark of the MI355X BitLinear hot path (one GPU).
+
+Workload (the metric's configuration): synthetic 1B-shape BitMamba-2 greedy
+decode, bs=1 -- 24 layers, d_model 2048, d_inner 4096, 64 heads of 64,
+in_proj 2048x8384 (the width the reference's loader accepts,
+src/model.c:683-701), out_proj 4096x2048, vocab 50257, ternary p(0)=0.4,
+fp32 parts N(0, 0.02), 8-token prompt.  A step is one decoded token, run as
+one replay of the captured per-token hipGraph with inputs already in HBM.
+
+Prints ONE JSON line.  Legs (all by default):
+  decode    W untimed steps, then K timed steps -> tok/s (the value) and
+            packed-weight GB/s
+  roofline  the decode GEMV kernel (K=2048 in_proj shape) streaming 512 MiB
+            of distinct weight rows in one launch, timed with HIP events on
+            the library stream -> achieved GB/s vs 8 TB/s
+  prefill   int8-MFMA GEMM at M=2048: 2048->8512 and 4096->2048, TOP/s
+  cpu       the reference's own AVX2 build (oracle/_ref) on the host cores:
+            a bounded sample of the same decode workload
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "bitmamba.c_amd"))
+import bitmamba_hip as bh  # noqa: E402
+
+METRIC = "packed-weight GB/s + tok/s (1B-shape decode, bs=1); prefill ternary GEMM TOPS"
+CFG_1B = dict(vocab=50257, d_model=2048, n_layers=24, n_heads=64, dist=bh.SYNTH_P0_40,
+              seed=1000, prompt=8)
+HBM_PEAK_GBPS = 8000.0
+I8_PEAK_TOPS = 5000.0
+
+
+def packed_bytes_per_token(c):
+    dm, di, nh = c["d_model"], 2 * c["d_model"], c["n_heads"]
+    pd = 2 * di + 3 * nh
+    return c["n_layers"] * (pd * dm // 4 + dm * di // 4) + c["vocab"] * dm // 4
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+class Events:
+    def __init__(self, L):
+        self.L = L
+        self.a, self.b = L.bm_hip_event_create(), L.bm_hip_event_create()
+
+    def start(self):
+        self.L.bm_hip_event_record(self.a, None)
+
+    def stop_ms(self):
+        self.L.bm_hip_event_record(self.b, None)
+        return self.L.bm_hip_event_elapsed_ms(self.a, self.b)
+
+
+def leg_decode(L, steps, warmup):
+    c = CFG_1B
+    t0 = time.time()
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          c["dist"])
+    prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
+    log("1B-shape image %.0f MB built in %.1fs" % (blob.nbytes / 1e6, time.time() - t0))
+    m = bh.Model(blob)
+    del blob
+    first, _ = m.generate(prompt, warmup)           # prefill + warmup steps (untimed)
+    L.bm_hip_synchronize()
+    t0 = time.perf_counter()
+    dev_ms = m.decode(steps)                         # K graph replays
+    L.bm_hip_synchronize()
+    wall = time.perf_counter() - t0
+    toks = np.concatenate([first, m.tokens(steps)])
+    m.free()
+    match = None
+    gold = os.path.join(ROOT, "tests", "golden", "stream_1b.json")
+    if os.path.exists(gold):
+        ref = json.load(open(gold))["tokens"]
+        n = min(len(ref), len(toks))
+        match = toks[:n].tolist() == ref[:n]
+    return wall, dev_ms, match
+
+
+def leg_roofline(L, reps=5):
+    K, N_layer = 2048, 2 * 4096 + 3 * 64              # in_proj 2048 -> 8384
+    row_bytes = K // 4
+    target = 512 << 20
+    n_layers_eq = (target + N_layer * row_bytes - 1) // (N_layer * row_bytes)
+    N = n_layers_eq * N_layer                         # stacked distinct rows, one launch
+    wbytes = N * row_bytes
+    w_host = bh.synth_ternary(7, 1, N, K, bh.SYNTH_P0_40)
+    dW = bh.DeviceBuffer.from_array(w_host)
+    del w_host
+    x = bh.synth_normal(7, 2, (1, K), 1.0)
+    g = np.ones(K, np.float32)
+    dx, dg = bh.DeviceBuffer.from_array(x), bh.DeviceBuffer.from_array(g)
+    dq, ds = bh.DeviceBuffer(K), bh.DeviceBuffer(4)
+    da = bh.DeviceBuffer(L.bm_hip_act_bytes(1, K))
+    dout = bh.DeviceBuffer(4 * N)
+    bh.check(L.bm_hip_quantize_dev(dx.ptr, 1, K, K, dg.ptr, None, dq.ptr, K, ds.ptr, da.ptr,
+                                   None), "quantize")
+    ev = Events(L)
+    for _ in range(2):                                # warm the code path
+        bh.check(L.bm_hip_bitlinear_act_dev(da.ptr, ds.ptr, 1, dW.ptr, N, K, 0.02, 1, dout.ptr,
+                                            None), "gemv")
+    ev.start()
+    for _ in range(reps):
+        bh.check(L.bm_hip_bitlinear_act_dev(da.ptr, ds.ptr, 1, dW.ptr, N, K, 0.02, 1, dout.ptr,
+                                            None), "gemv")
+    ms = ev.stop_ms() / reps
+    achieved = wbytes / (ms * 1e-3) / 1e9
+    for b in (dW, dx, dg, dq, ds, da, dout):
+        b.free()
+    return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
+                kernel="k_gemv<32,1,2,canonical,store> (K=2048 decode GEMV)",
+                bytes_per_launch=wbytes, launch_us=round(ms * 1e3, 2),
+                rows_per_launch=N)
+
+
+def leg_prefill(L, reps=10):
+    out = {}
+    ev = Events(L)
+    for K, N in ((2048, 8512), (4096, 2048)):
+        M = 2048
+        w = bh.synth_ternary(11, 1, N, K, bh.SYNTH_UNIFORM)
+        x = bh.synth_normal(11, 2, (M, K), 1.0)
+        dW, dx = bh.DeviceBuffer.from_array(w), bh.DeviceBuffer.from_array(x)
+        dg = bh.DeviceBuffer.from_array(np.ones(K, np.float32))
+        dq, ds = bh.DeviceBuffer(M * K), bh.DeviceBuffer(4 * M)
+        da = bh.DeviceBuffer(L.bm_hip_act_bytes(M, K))
+        dout = bh.DeviceBuffer(4 * M * N)
+        bh.check(L.bm_hip_quantize_dev(dx.ptr, M, K, K, dg.ptr, None, dq.ptr, K, ds.ptr, da.ptr,
+                                       None), "quantize")
+        bh.check(L.bm_hip_bitlinear_act_dev(da.ptr, ds.ptr, M, dW.ptr, N, K, 0.02, 1, dout.ptr,
+                                            None), "gemm")
+        ev.start()
+        for _ in range(reps):
+            bh.check(L.bm_hip_bitlinear_act_dev(da.ptr, ds.ptr, M, dW.ptr, N, K, 0.02, 1,
+                                                dout.ptr, None), "gemm")
+        ms = ev.stop_ms() / reps
+        ev.start()
+        for _ in range(reps):
+            bh.check(L.bm_hip_quantize_dev(dx.ptr, M, K, K, dg.ptr, None, dq.ptr, K, ds.ptr,
+                                           da.ptr, None), "quantize")
+        qms = ev.stop_ms() / reps
+        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out["%dx%dx%d" % (M, K, N)] = dict(gemm_us=round(ms * 1e3, 1), tops=round(tops, 1),
+                                           frac=round(tops * 1e3 / I8_PEAK_TOPS, 4),
+                                           quantize_us=round(qms * 1e3, 1))
+        for b in (dW, dx, dg, dq, ds, da, dout):
+            b.free()
+    return out
+
+
+def leg_cpu(sample_tokens=48):
+    """The reference's own C (oracle/_ref: dispatch_init -> AVX2+FMA kernels,
+    its thread pool) decoding the same synthetic 1B-shape model."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import native
+    if not native.ref_available():
+        return None
+    R = native.ref()
+    threads = min(os.cpu_count() or 1, 16)
+    name = R.bmref_init(threads, 1).decode()
+    R.bmref_set_poll(100)                            # the reference's default wait policy
+    c = CFG_1B
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          c["dist"])
+    prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    with tempfile.NamedTemporaryFile(suffix=".bin", dir=d) as f:
+        blob.tofile(f.name)
+        del blob
+        h = R.bmref_model_load(f.name.encode())
+        p = np.ascontiguousarray(prompt[:-1], np.int32)
+        R.bmref_model_prefill(h, native.ptr(p), p.size)
+        hist = [int(t) for t in prompt]
+        cur = int(prompt[-1])
+        times = []
+        for _ in range(sample_tokens):
+            harr = np.array(hist[-256:], np.int32)
+            t0 = time.perf_counter()
+            cur = R.bmref_model_step(h, cur, native.ptr(harr), harr.size, 1.0)
+            times.append(time.perf_counter() - t0)
+            hist.append(cur)
+        R.bmref_model_free(h)
+    R.bmref_shutdown()
+    tok_s = len(times) / sum(times)
+    return dict(value=round(tok_s, 2), unit="tok/s", cores=threads, kind="reference",
+                sample="%d greedy steps of the same 1B-shape decode after a 7-token prefill "
+                       "(reference kernels: %s, %d threads)" % (sample_tokens, name, threads))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--legs", default="decode,roofline,prefill,cpu")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on exactly one GPU (the BitLinear hot path at bs=1 "
+              "has no multi-GPU path); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    legs = set(a.legs.split(","))
+    L = bh.lib()
+    if not L.bm_hip_init():
+        sys.exit("bm_hip_init: " + bh.last_error())
+    res = {}
+    if "decode" in legs:
+        wall, dev_ms, match = leg_decode(L, a.steps, a.warmup)
+        res["decode"] = (wall, dev_ms, match)
+        log("decode: %d steps in %.2f ms wall (%.2f ms device)" % (a.steps, wall * 1e3, dev_ms))
+    roof = leg_roofline(L) if "roofline" in legs else None
+    if roof:
+        log("roofline: %.1f GB/s (%.1f%% of HBM peak), %.1f us per launch"
+            % (roof["achieved"], 100 * roof["frac"], roof["launch_us"]))
+    pre = leg_prefill(L) if "prefill" in legs else None
+    if pre:
+        log("prefill: %s" % json.dumps(pre))
+    cpu = leg_cpu() if "cpu" in legs else None
+    if cpu:
+        log("cpu baseline: %s" % json.dumps(cpu))
+
+    bpt = packed_bytes_per_token(CFG_1B)
+    line = {"metric": METRIC, "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": "1B-shape BitMamba-2 greedy decode, bs=1 (24 layers, "
+                                   "d_model 2048, d_inner 4096, 64 heads, in_proj 2048x8384, "
+                                   "out_proj 4096x2048, vocab 50257, ternary p0=0.4)",
+                       "prompt_tokens": CFG_1B["prompt"], "seed": CFG_1B["seed"],
+                       "parallelism": "single GPU"}}
+    if "decode" in res:
+        wall, dev_ms, match = res["decode"]
+        tok_s = a.steps / wall
+        line.update(value=round(tok_s, 2), ms_per_step=round(wall * 1e3 / a.steps, 4),
+                    packed_weight_GBps=round(tok_s * bpt / 1e9, 1),
+                    packed_bytes_per_token=bpt, device_ms_per_step=round(dev_ms / a.steps, 4),
+                    tokens_match_reference=match)
+    else:
+        line.update(value=None, ms_per_step=None)
+    line["roofline"] = roof
+    line["prefill_gemm"] = pre
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -58,6 +58,12 @@ SIGNATURES = {
     "bm_hip_memset": (_i, [_vp, _i, _sz]),
     "bm_hip_synchronize": (_i, []),
     "bm_hip_canonicalize_dev": (_i, [_vp, _sz, _vp]),
+    "bm_hip_stream": (_vp, []),
+    "bm_hip_event_create": (_vp, []),
+    "bm_hip_event_destroy": (None, [_vp]),
+    "bm_hip_event_record": (_i, [_vp, _vp]),
+    "bm_hip_event_elapsed_ms": (_f, [_vp, _vp]),
+    "bm_hip_copy_dev": (_i, [_vp, _vp, _sz, _vp]),
     "bm_hip_act_bytes": (_sz, [_i, _i]),
     "bm_hip_quantize_dev": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "bm_hip_bitlinear_act_dev": (_i, [_vp, _vp, _i, _vp, _i, _i, _f, _i, _vp, _vp]),
@@ -65,6 +71,18 @@ SIGNATURES = {
                                   _vp]),
     "bm_hip_i8_act_bytes": (_sz, [_i, _i]),
     "bm_hip_ternary_gemm_i32_dev": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "bm_hip_model_load": (_vp, [_vp, _sz]),
+    "bm_hip_model_free": (None, [_vp]),
+    "bm_hip_model_config": (_i, [_vp, _i]),
+    "bm_hip_model_reset": (_i, [_vp]),
+    "bm_hip_model_prefill": (_i, [_vp, _vp, _i]),
+    "bm_hip_model_step": (_i, [_vp, _i, _vp, _i, _f]),
+    "bm_hip_model_logits": (_i, [_vp, _vp]),
+    "bm_hip_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
+    "bm_hip_model_generate": (_i, [_vp, _vp, _i, _i, _f, _i, _vp, C.POINTER(C.c_double)]),
+    "bm_hip_model_decode": (_i, [_vp, _i, _f, C.POINTER(C.c_double)]),
+    "bm_hip_model_tokens": (_i, [_vp, _vp, _i]),
+    "bm_hip_libm_eval_dev": (_i, [_i, _vp, _vp, _sz, _vp]),
     "bm_bit2_synth_size": (_sz, [C.POINTER(SynthConfig)]),
     "bm_bit2_synth_write": (_i, [C.POINTER(SynthConfig), _vp, _sz]),
     "bm_synth_ternary": (None, [_u64, _i, _i, _i, _i, _vp]),
@@ -200,3 +218,72 @@ def make_tensor(packed=None, rows=0, cols=0, scale=1.0, data=None):
         t.n_elements = data.size
         t.scale = 1.0
     return t
+
+
+class Model:
+    """Device-resident model loaded from a BIT2 image (numpy uint8 array)."""
+
+    def __init__(self, image):
+        self.image = image  # the library copies it; kept for the caller's convenience
+        self.h = lib().bm_hip_model_load(ptr(image), image.nbytes)
+        if not self.h:
+            raise RuntimeError("bm_hip_model_load: " + last_error())
+        L = lib()
+        self.vocab, self.d_model, self.n_layers, self.n_heads, self.d_inner = (
+            L.bm_hip_model_config(self.h, i) for i in range(5))
+
+    def generate(self, prompt, n_steps, penalty=1.0, stop_on_eos=False):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(max(n_steps, 1), np.int32)
+        ms = C.c_double(0.0)
+        n = lib().bm_hip_model_generate(self.h, ptr(prompt), prompt.size, n_steps, penalty,
+                                        int(stop_on_eos), ptr(out), C.byref(ms))
+        if n < 0:
+            raise RuntimeError("generate: " + last_error())
+        return out[:n].copy(), ms.value
+
+    def prefill(self, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        check(lib().bm_hip_model_prefill(self.h, ptr(tokens), tokens.size), "prefill")
+
+    def step(self, token, history, penalty=1.0):
+        h = np.ascontiguousarray(history, dtype=np.int32)
+        r = lib().bm_hip_model_step(self.h, int(token), ptr(h), h.size, penalty)
+        if r < 0:
+            raise RuntimeError("step: " + last_error())
+        return r
+
+    def logits(self):
+        out = np.empty(self.vocab, np.float32)
+        check(lib().bm_hip_model_logits(self.h, ptr(out)), "logits")
+        return out
+
+    def layer_state(self, layer):
+        cs = np.empty((3, self.d_inner), np.float32)
+        ss = np.empty(self.d_inner, np.float32)
+        pos = lib().bm_hip_model_layer_state(self.h, layer, ptr(cs), ptr(ss))
+        return cs, ss, pos
+
+    def decode(self, n_steps, penalty=1.0):
+        ms = C.c_double(0.0)
+        check(lib().bm_hip_model_decode(self.h, n_steps, penalty, C.byref(ms)), "decode")
+        return ms.value
+
+    def tokens(self, n):
+        out = np.empty(n, np.int32)
+        n = lib().bm_hip_model_tokens(self.h, ptr(out), n)
+        return out[:n]
+
+    def reset(self):
+        check(lib().bm_hip_model_reset(self.h), "reset")
+
+    def free(self):
+        if self.h:
+            lib().bm_hip_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

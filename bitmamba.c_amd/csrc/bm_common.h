@@ -52,12 +52,21 @@ hipError_t launch_quantize(const float *x, int M, int n, int x_stride,
                            hipStream_t s);
 hipError_t launch_prep_i8(const int8_t *xq, int M, int ldx, int K, uint8_t *act,
                           hipStream_t s);
+// Output modes of the products: fp32 store, fp32 accumulate (out += o, the
+// residual add of src/model.c:1214-1215, 1139-1142), exact int32 totals.
+enum { MODE_STORE = 0, MODE_ACC = 1, MODE_I32 = 2 };
+
 // fp32 output with the scalar 1024-column epilogue; inv[m] computed from
-// scale_x[m] and w_scale (scale_x == nullptr -> int32 totals into out_i32)
+// scale_x[m] and w_scale (unused for MODE_I32)
 hipError_t launch_product(const uint8_t *act, const float *scale_x, int M,
                           const uint8_t *packed, int N, int K, float w_scale,
-                          bool canonical, float *out, int32_t *out_i32,
-                          hipStream_t s);
+                          bool canonical, void *out, int mode, hipStream_t s);
+bool product_needs_generic(int M, int K);
+hipError_t launch_generic(const int8_t *xq, int ldx, const float *scale_x,
+                          int M, const uint8_t *packed, int N, int K,
+                          float w_scale, void *out, int mode, hipStream_t s);
+hipError_t launch_rms_norm(const float *x, int n, const float *gamma,
+                           float *out, float *max_out, hipStream_t s);
 hipError_t launch_canonicalize(uint8_t *p, size_t bytes, hipStream_t s);
 
 }  // namespace bm

@@ -14,6 +14,7 @@
 // code 11 is rewritten to 10 first (same value) unless the caller promises
 // canonical weights.
 #include "bm_common.h"
+#include "bm_fp.h"
 
 namespace bm {
 
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(QT) void k_quantize(const float* __restrict__ x, in
   if (tid == 0) {
     float sum = __fadd_rn(__fadd_rn(__fadd_rn(s_chain[0], s_chain[1]), s_chain[2]), s_chain[3]);
     for (int i = n4; i < n; ++i) sum = __fadd_rn(sum, __fmul_rn(xr[i], xr[i]));
-    s_rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)n), 1e-6f)));
+    s_rms = cr_divf(1.0f, cr_sqrtf(__fadd_rn(cr_divf(sum, (float)n), 1e-6f)));
   }
   __syncthreads();
   const float rms = s_rms;
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(QT) void k_quantize(const float* __restrict__ x, in
 #pragma unroll
   for (int w = 1; w < QT / 64; ++w) max_abs = fmaxf(max_abs, s_wmax[w]);
 
-  const float scale_x = __fdiv_rn(127.0f, __fadd_rn(max_abs, 1e-5f));
+  const float scale_x = cr_divf(127.0f, __fadd_rn(max_abs, 1e-5f));
   if (tid == 0) {
     if (scale_out) scale_out[m] = scale_x;
     if (max_out) max_out[m] = max_abs;
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(QT) void k_prep_i8(const int8_t* __restrict__ xq, i
 }
 
 __device__ __forceinline__ float inv_scale_of(float scale_x, float w_scale) {
-  return __fdiv_rn(1.0f, __fmul_rn(scale_x, w_scale));  // src/kernel.c:391
+  return cr_divf(1.0f, __fmul_rn(scale_x, w_scale));  // src/kernel.c:391
 }
 
 // ---------------------------------------------------------------------------
@@ -212,12 +213,13 @@ __device__ __forceinline__ float inv_scale_of(float scale_x, float w_scale) {
 //   per pass; P passes cover K.  16 consecutive lanes = one 1024-column
 //   slice, reduced with xor shuffles inside the 16-lane group.
 // ---------------------------------------------------------------------------
-template <int T, int P, int UNR, bool CANON, bool I32>
+template <int T, int P, int UNR, bool CANON, int MODE>
 __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, size_t act_stride,
                                               const float* __restrict__ scale_x,
                                               const uint8_t* __restrict__ W, int N, int K,
                                               float w_scale, float* __restrict__ out,
                                               int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
   constexpr int RPW = 64 / T;  // rows per wave per row-group
   const int m = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -245,7 +247,9 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, s
       xa[p][4 * g + 2] = v.z;
       xa[p][4 * g + 3] = v.w;
     }
-    xs[p] = ssum[(p * T + u) / 16 < slices_of(K) ? (p * T + u) / 16 : 0];
+    // lane groups past the last slice hold no columns: their total is 0
+    const int slice = (p * T + u) / 16;
+    xs[p] = slice < slices_of(K) ? ssum[slice] : 0;
   }
   const float inv = I32 ? 0.0f : inv_scale_of(scale_x[m], w_scale);
 
@@ -309,7 +313,8 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, s
         if (I32)
           out_i32[(size_t)m * N + rows[i]] = tot;
         else
-          out[(size_t)m * N + rows[i]] = o;
+          out[(size_t)m * N + rows[i]] =
+              MODE == 1 ? __fadd_rn(out[(size_t)m * N + rows[i]], o) : o;
       }
     }
   }
@@ -319,12 +324,13 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, s
 // Generic product for any K (K % 64 != 0 or very long rows): one wave per
 // row, plain int8 activations, 1024-column slices then the K % 4 remainder.
 // ---------------------------------------------------------------------------
-template <bool I32>
+template <int MODE>
 __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, int ldx,
                                                  const float* __restrict__ scale_x,
                                                  const uint8_t* __restrict__ W, int N, int K,
                                                  float w_scale, float* __restrict__ out,
                                                  int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
   const int m = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -370,7 +376,7 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
     if (I32)
       out_i32[(size_t)m * N + r] = tot;
     else
-      out[(size_t)m * N + r] = o;
+      out[(size_t)m * N + r] = MODE == 1 ? __fadd_rn(out[(size_t)m * N + r], o) : o;
   }
 }
 
@@ -386,12 +392,13 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 // ---------------------------------------------------------------------------
 constexpr int GBM = 128, GBN = 128, GBK = 128, GLDA = GBK + 16;
 
-template <bool CANON, bool I32>
+template <bool CANON, int MODE>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ act, size_t act_stride,
                                               const float* __restrict__ scale_x, int M,
                                               const uint8_t* __restrict__ W, int N, int K,
                                               float w_scale, float* __restrict__ out,
                                               int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
   __shared__ __attribute__((aligned(16))) int8_t sA[GBM * GLDA];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -496,7 +503,8 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ act, s
           if (I32)
             out_i32[(size_t)r * N + n] = __float_as_int(o[mt][nt][v]);
           else
-            out[(size_t)r * N + n] = o[mt][nt][v];
+            out[(size_t)r * N + n] =
+                MODE == 1 ? __fadd_rn(out[(size_t)r * N + n], o[mt][nt][v]) : o[mt][nt][v];
         }
       }
     }
@@ -538,9 +546,9 @@ hipError_t launch_prep_i8(const int8_t* xq, int M, int ldx, int K, uint8_t* act,
   return hipGetLastError();
 }
 
-template <int T, int P, bool CANON, bool I32>
+template <int T, int P, bool CANON, int MODE>
 static hipError_t gemv_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
-                         int K, float w_scale, float* out, int32_t* out_i32, hipStream_t s) {
+                         int K, float w_scale, void* out, hipStream_t s) {
   constexpr int RPW = 64 / T;
   const int n_rg = (N + RPW - 1) / RPW;
   const int UNR = 2;
@@ -548,28 +556,27 @@ static hipError_t gemv_t(const uint8_t* act, const float* scale_x, int M, const 
   int blocks = (waves + 3) / 4;
   const int cap = 2048;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL((k_gemv<T, P, 2, CANON, I32>), dim3(blocks, M), dim3(256), 0, s, act,
-                     act_row_bytes(K), scale_x, W, N, K, w_scale, out, out_i32);
+  hipLaunchKernelGGL((k_gemv<T, P, 2, CANON, MODE>), dim3(blocks, M), dim3(256), 0, s, act,
+                     act_row_bytes(K), scale_x, W, N, K, w_scale, (float*)out, (int32_t*)out);
   return hipGetLastError();
 }
 
-template <bool CANON, bool I32>
+template <bool CANON, int MODE>
 static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
-                                int N, int K, float w_scale, float* out, int32_t* out_i32,
-                                hipStream_t s) {
-  if (K <= 1024) return gemv_t<16, 1, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
-  if (K <= 2048) return gemv_t<32, 1, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
-  if (K <= 4096) return gemv_t<64, 1, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
-  if (K <= 8192) return gemv_t<64, 2, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
-  return gemv_t<64, 4, CANON, I32>(act, scale_x, M, W, N, K, w_scale, out, out_i32, s);
+                                int N, int K, float w_scale, void* out, hipStream_t s) {
+  if (K <= 1024) return gemv_t<16, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  if (K <= 2048) return gemv_t<32, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  if (K <= 4096) return gemv_t<64, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  if (K <= 8192) return gemv_t<64, 2, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  return gemv_t<64, 4, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
 }
 
-template <bool CANON, bool I32>
+template <bool CANON, int MODE>
 static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
-                         int K, float w_scale, float* out, int32_t* out_i32, hipStream_t s) {
+                         int K, float w_scale, void* out, hipStream_t s) {
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
-  hipLaunchKernelGGL((k_gemm<CANON, I32>), grid, dim3(256), 0, s, act, act_row_bytes(K), scale_x,
-                     M, W, N, K, w_scale, out, out_i32);
+  hipLaunchKernelGGL((k_gemm<CANON, MODE>), grid, dim3(256), 0, s, act, act_row_bytes(K), scale_x,
+                     M, W, N, K, w_scale, (float*)out, (int32_t*)out);
   return hipGetLastError();
 }
 
@@ -580,40 +587,44 @@ static int product_path(int M, int K) {
   return 1;                                // GEMV per token
 }
 
+template <bool CANON, int MODE>
+static hipError_t product_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
+                            int N, int K, float w_scale, void* out, hipStream_t s) {
+  if (product_path(M, K) == 2) return gemm_t<CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  return gemv_dispatch<CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+}
+
 hipError_t launch_product(const uint8_t* act, const float* scale_x, int M, const uint8_t* packed,
-                          int N, int K, float w_scale, bool canonical, float* out,
-                          int32_t* out_i32, hipStream_t s) {
-  const bool i32 = out_i32 != nullptr;
-  switch (product_path(M, K)) {
-    case 2:
-      if (canonical)
-        return i32 ? gemm_t<true, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
-                   : gemm_t<true, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
-      return i32 ? gemm_t<false, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
-                 : gemm_t<false, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
-    case 1:
-      if (canonical)
-        return i32 ? gemv_dispatch<true, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
-                   : gemv_dispatch<true, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
-      return i32 ? gemv_dispatch<false, true>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s)
-                 : gemv_dispatch<false, false>(act, scale_x, M, packed, N, K, w_scale, out, out_i32, s);
-    default:
-      return hipErrorInvalidValue;  // caller uses launch_generic
+                          int N, int K, float w_scale, bool canonical, void* out, int mode,
+                          hipStream_t s) {
+  if (product_path(M, K) == 0) return hipErrorInvalidValue;  // caller uses launch_generic
+  if (canonical) {
+    if (mode == MODE_I32) return product_t<true, 2>(act, scale_x, M, packed, N, K, w_scale, out, s);
+    if (mode == MODE_ACC) return product_t<true, 1>(act, scale_x, M, packed, N, K, w_scale, out, s);
+    return product_t<true, 0>(act, scale_x, M, packed, N, K, w_scale, out, s);
   }
+  if (mode == MODE_I32) return product_t<false, 2>(act, scale_x, M, packed, N, K, w_scale, out, s);
+  if (mode == MODE_ACC) return product_t<false, 1>(act, scale_x, M, packed, N, K, w_scale, out, s);
+  return product_t<false, 0>(act, scale_x, M, packed, N, K, w_scale, out, s);
 }
 
 bool product_needs_generic(int M, int K) { return product_path(M, K) == 0; }
 
 hipError_t launch_generic(const int8_t* xq, int ldx, const float* scale_x, int M,
-                          const uint8_t* packed, int N, int K, float w_scale, float* out,
-                          int32_t* out_i32, hipStream_t s) {
+                          const uint8_t* packed, int N, int K, float w_scale, void* out, int mode,
+                          hipStream_t s) {
   dim3 grid((N + 3) / 4, M);
-  if (out_i32)
-    hipLaunchKernelGGL(k_generic<true>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
-                       w_scale, out, out_i32);
+  float* of = (float*)out;
+  int32_t* oi = (int32_t*)out;
+  if (mode == MODE_I32)
+    hipLaunchKernelGGL(k_generic<2>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
+                       w_scale, of, oi);
+  else if (mode == MODE_ACC)
+    hipLaunchKernelGGL(k_generic<1>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
+                       w_scale, of, oi);
   else
-    hipLaunchKernelGGL(k_generic<false>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
-                       w_scale, out, out_i32);
+    hipLaunchKernelGGL(k_generic<0>, grid, dim3(256), 0, s, xq, ldx, scale_x, packed, N, K,
+                       w_scale, of, oi);
   return hipGetLastError();
 }
 

@@ -1,0 +1,682 @@
+// Device-resident BitMamba model: the reference's model_load /
+// model_prefill / model_forward_step (src/model.c:477-1314, src/block.c)
+// with every activation kept in HBM.
+//
+// Per decoded token the device runs, without a host round trip:
+//   embed -> per layer [quantize x; in_proj GEMV; SSM step; quantize y;
+//   out_proj GEMV accumulated into x] -> RMSNorm(norm_f) -> quantize ->
+//   LM-head GEMV -> repetition penalty -> greedy argmax.
+// The sequence is captured once into a hipGraph and replayed; the current
+// token, conv ring position, step counter and history live in device memory.
+// Numerics are those of the scalar reference path, bit for bit.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "bm_bit2.h"
+#include "bm_common.h"
+#include "bm_fp.h"
+#include "bm_hip.h"
+#include "bm_libm.h"
+
+namespace bm {
+
+// control block in device memory
+enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_WORDS = 8 };
+constexpr int kHistory = 256;  // HISTORY_MAX (src/main.c:19)
+
+__device__ __forceinline__ float silu_ref(float x) {
+  // x / (1.0f + expf(-x))  (src/bitmamba.h:234-237)
+  return cr_divf(x, __fadd_rn(1.0f, libm::expf_glibc(-x)));
+}
+
+__device__ __forceinline__ float softplus_ref(float x) {
+  // x > 20 ? x : logf(1.0f + expf(x))  (src/bitmamba.h:238-243)
+  if (x > 20.0f) return x;
+  return libm::logf_glibc(__fadd_rn(1.0f, libm::expf_glibc(x)));
+}
+
+// One channel of scalar_ssm_inner (src/kernel.c:34-70) for one token.
+__device__ __forceinline__ void ssm_channel(const float* __restrict__ proj, int di, int nh, int hd,
+                                            int idx, int pos, const float* __restrict__ dt_bias,
+                                            const float* __restrict__ A,
+                                            const float* __restrict__ cw,
+                                            const float* __restrict__ cb,
+                                            float* __restrict__ cs, float* __restrict__ ssm,
+                                            const float* __restrict__ D, float* __restrict__ y) {
+  const int h = idx / hd;
+  const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
+  const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
+  const float dt_val = softplus_ref(__fadd_rn(proj[2 * di + 2 * nh + h], dt_bias[h]));
+  const float decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
+  const float Bdt = __fmul_rn(proj[2 * di + h], dt_val);
+  const float C_val = proj[2 * di + nh + h];
+  const float xin = proj[di + idx];
+  float* c0 = cs + (size_t)pos * di;
+  float conv = __fadd_rn(cb[idx], __fmul_rn(c0[idx], cw[idx]));
+  conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t1 * di + idx], cw[di + idx]));
+  conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t2 * di + idx], cw[2 * di + idx]));
+  conv = __fadd_rn(conv, __fmul_rn(xin, cw[3 * di + idx]));
+  c0[idx] = xin;  // the oldest tap is overwritten (cs_write == cs0)
+  const float xa = silu_ref(conv);
+  const float st = __fadd_rn(__fmul_rn(ssm[idx], decay), __fmul_rn(xa, Bdt));
+  ssm[idx] = st;
+  y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xa, D[idx])), silu_ref(proj[idx]));
+}
+
+__global__ void k_ssm_step(const float* __restrict__ proj, int di, int nh, int hd,
+                           const float* __restrict__ dt_bias, const float* __restrict__ A,
+                           const float* __restrict__ cw, const float* __restrict__ cb,
+                           float* __restrict__ cs, float* __restrict__ ssm,
+                           const float* __restrict__ D, float* __restrict__ y,
+                           const int* __restrict__ ctl) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= di) return;
+  ssm_channel(proj, di, nh, hd, idx, ctl[CTL_POS], dt_bias, A, cw, cb, cs, ssm, D, y);
+}
+
+// n tokens in order; each thread owns one channel across all tokens
+// (ssm_batch_worker, src/block.c:127-160)
+__global__ void k_ssm_batch(const float* __restrict__ proj, int pd, int n, int di, int nh, int hd,
+                            const float* __restrict__ dt_bias, const float* __restrict__ A,
+                            const float* __restrict__ cw, const float* __restrict__ cb,
+                            float* __restrict__ cs, float* __restrict__ ssm,
+                            const float* __restrict__ D, float* __restrict__ y,
+                            const int* __restrict__ ctl) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= di) return;
+  int pos = ctl[CTL_POS];
+  for (int t = 0; t < n; ++t) {
+    ssm_channel(proj + (size_t)t * pd, di, nh, hd, idx, pos, dt_bias, A, cw, cb, cs, ssm, D,
+                y + (size_t)t * di);
+    pos = pos + 1 < 3 ? pos + 1 : 0;
+  }
+}
+
+__global__ void k_advance_pos(int* ctl, int n) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) ctl[CTL_POS] = (ctl[CTL_POS] + n) % 3;
+}
+
+// x[t] = embed[tok[t]]; out-of-range ids read row 0 (src/model.c:1116-1122)
+__global__ void k_embed(const float* __restrict__ embed, int dm, int vocab,
+                        const int* __restrict__ toks, float* __restrict__ x) {
+  const int t = blockIdx.y;
+  int tok = toks[t];
+  if (tok < 0 || tok >= vocab) tok = 0;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dm; i += gridDim.x * blockDim.x)
+    x[(size_t)t * dm + i] = embed[(size_t)tok * dm + i];
+}
+
+// A_precomp = -expf(A_log) (src/model.c:786-792)
+__global__ void k_neg_exp(const float* __restrict__ a, float* __restrict__ out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = -libm::expf_glibc(a[i]);
+}
+
+// Repetition penalty over the distinct tokens of the last kHistory
+// (src/model.c:1272-1305).  Each distinct token is scaled once, so the
+// entries can be processed in parallel.
+__global__ void k_penalty(float* __restrict__ logits, int vocab, const int* __restrict__ hist,
+                          const int* __restrict__ ctl, float penalty) {
+  const int count = ctl[CTL_HCOUNT];
+  const int len = count < kHistory ? count : kHistory;
+  const int j = threadIdx.x;
+  if (j >= len) return;
+  const int base = count - len;
+  const int past = hist[(base + j) % kHistory];
+  if (past < 0 || past >= vocab) return;
+  for (int i = 0; i < j; ++i)
+    if (hist[(base + i) % kHistory] == past) return;  // not the first occurrence
+  if (past == 50256 || past == 198 || past == 628 || past == 13) return;
+  if (!(penalty > 0.0f)) return;
+  const float v = logits[past];
+  logits[past] = v > 0 ? cr_divf(v, penalty) : __fmul_rn(v, penalty);
+}
+
+// Greedy pick: first index of the maximum, starting from best = 0 and
+// max = -1e9 (src/model.c:143-154).  Then bookkeeping for the next step.
+__global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ logits, int vocab,
+                                                       int* __restrict__ ctl,
+                                                       int* __restrict__ hist,
+                                                       int* __restrict__ out_tokens) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  float bv = -1e9f;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+    const float v = logits[i];
+    if (v > bv) {  // ascending i per thread: first max kept
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    const int best = bi == 0x7fffffff ? 0 : bi;
+    const int step = ctl[CTL_STEP];
+    if (out_tokens) out_tokens[step] = best;
+    ctl[CTL_STEP] = step + 1;
+    ctl[CTL_TOKEN] = best;
+    hist[ctl[CTL_HCOUNT] % kHistory] = best;
+    ctl[CTL_HCOUNT] += 1;
+    ctl[CTL_POS] = ctl[CTL_POS] + 1 < 3 ? ctl[CTL_POS] + 1 : 0;  // src/block.c:107
+  }
+}
+
+}  // namespace bm
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Layer {
+  float *in_norm, *conv_wt, *conv_b, *dt_bias, *A, *D, *out_norm;
+  uint8_t *in_proj, *out_proj;
+  float in_scale, out_scale;
+};
+
+}  // namespace
+
+struct bm_hip_model {
+  int vocab = 0, dm = 0, nl = 0, nh = 0, di = 0, hd = 0, pd = 0;
+  hipStream_t stream = nullptr;
+  void* arena = nullptr;  // every weight, 256-byte aligned sub-buffers
+  size_t arena_bytes = 0;
+  float* embed = nullptr;
+  float *norm_f = nullptr, *lm_norm = nullptr;
+  uint8_t* lm_head = nullptr;
+  float lm_scale = 1.0f;
+  std::vector<Layer> L;
+  // state
+  float *conv_state = nullptr, *ssm_state = nullptr;
+  int *ctl = nullptr, *hist = nullptr, *out_tokens = nullptr;
+  int out_cap = 0;
+  // decode scratch
+  float *x = nullptr, *proj = nullptr, *y = nullptr, *feat = nullptr, *logits = nullptr;
+  float* scale = nullptr;
+  uint8_t* act = nullptr;
+  int8_t* xq = nullptr;
+  // prefill scratch (grow on demand)
+  float *px = nullptr, *pproj = nullptr, *py = nullptr, *pscale = nullptr;
+  uint8_t* pact = nullptr;
+  int8_t* pxq = nullptr;
+  int* ptok = nullptr;
+  int pcap = 0;
+  // captured decode step
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  float graph_penalty = 1.0f;
+  bool graph_with_out = false;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace {
+
+#define MCHECK(expr)                                                                     \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess) {                                                              \
+      bm_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__,       \
+                   __LINE__);                                                            \
+      return -1;                                                                         \
+    }                                                                                    \
+  } while (0)
+
+size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// quantize + product of one BitLinear on M rows (src/kernel.c:346-448)
+int bitlinear(bm_hip_model* m, const float* x, int M, int K, const float* norm,
+              const uint8_t* W, int N, float scale, void* out, int mode, uint8_t* act,
+              float* sc, int8_t* xq, hipStream_t s) {
+  const bool generic = bm::product_needs_generic(M, K);
+  MCHECK(bm::launch_quantize(x, M, K, K, norm, nullptr, generic ? xq : nullptr, K, sc,
+                             generic ? nullptr : act, s));
+  if (generic)
+    MCHECK(bm::launch_generic(xq, K, sc, M, W, N, K, scale, out, mode, s));
+  else
+    MCHECK(bm::launch_product(act, sc, M, W, N, K, scale, true, out, mode, s));
+  (void)m;
+  return 0;
+}
+
+// The kernels of one decode step, enqueued on s.
+int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) {
+  const int dm = m->dm, di = m->di;
+  hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, 1), dim3(256), 0, s, m->embed, dm,
+                     m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
+  MCHECK(hipGetLastError());
+  for (int l = 0; l < m->nl; ++l) {
+    const Layer& Ly = m->L[l];
+    float* cs = m->conv_state + (size_t)l * 3 * di;
+    float* ss = m->ssm_state + (size_t)l * di;
+    if (bitlinear(m, m->x, 1, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
+                  bm::MODE_STORE, m->act, m->scale, m->xq, s))
+      return -1;
+    hipLaunchKernelGGL(bm::k_ssm_step, dim3((di + 255) / 256), dim3(256), 0, s, m->proj, di,
+                       m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
+                       m->ctl);
+    MCHECK(hipGetLastError());
+    if (bitlinear(m, m->y, 1, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x,
+                  bm::MODE_ACC, m->act, m->scale, m->xq, s))
+      return -1;
+  }
+  // final RMSNorm (src/model.c:1225), then the LM head BitLinear with its own
+  // norm (src/model.c:1259-1261)
+  MCHECK(bm::launch_rms_norm(m->x, dm, m->norm_f, m->feat, nullptr, s));
+  if (bitlinear(m, m->feat, 1, dm, m->lm_norm, m->lm_head, m->vocab, m->lm_scale, m->logits,
+                bm::MODE_STORE, m->act, m->scale, m->xq, s))
+    return -1;
+  if (penalty != 1.0f) {
+    hipLaunchKernelGGL(bm::k_penalty, dim3(1), dim3(bm::kHistory), 0, s, m->logits, m->vocab,
+                       m->hist, m->ctl, penalty);
+    MCHECK(hipGetLastError());
+  }
+  hipLaunchKernelGGL(bm::k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, m->vocab, m->ctl,
+                     m->hist, write_out ? m->out_tokens : nullptr);
+  MCHECK(hipGetLastError());
+  return 0;
+}
+
+int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
+  if (m->exec && m->graph_penalty == penalty && m->graph_with_out == write_out) return 0;
+  if (m->exec) {
+    (void)hipGraphExecDestroy(m->exec);
+    m->exec = nullptr;
+  }
+  if (m->graph) {
+    (void)hipGraphDestroy(m->graph);
+    m->graph = nullptr;
+  }
+  MCHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_step(m, m->stream, penalty, write_out);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(m->stream, &g);
+  if (rc != 0) {
+    if (g) (void)hipGraphDestroy(g);
+    return -1;
+  }
+  MCHECK(e);
+  m->graph = g;
+  MCHECK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+  m->graph_penalty = penalty;
+  m->graph_with_out = write_out;
+  return 0;
+}
+
+int ensure_prefill(bm_hip_model* m, int n) {
+  if (n <= m->pcap) return 0;
+  for (void* p : {(void*)m->px, (void*)m->pproj, (void*)m->py, (void*)m->pscale,
+                  (void*)m->pact, (void*)m->pxq, (void*)m->ptok})
+    if (p) (void)hipFree(p);
+  const size_t K = (size_t)(m->di > m->dm ? m->di : m->dm);
+  MCHECK(hipMalloc(&m->px, (size_t)n * m->dm * 4));
+  MCHECK(hipMalloc(&m->pproj, (size_t)n * m->pd * 4));
+  MCHECK(hipMalloc(&m->py, (size_t)n * m->di * 4));
+  MCHECK(hipMalloc(&m->pscale, (size_t)n * 4));
+  MCHECK(hipMalloc(&m->pact, (size_t)n * bm::act_row_bytes((int)K)));
+  MCHECK(hipMalloc(&m->pxq, (size_t)n * K));
+  MCHECK(hipMalloc(&m->ptok, (size_t)n * 4));
+  m->pcap = n;
+  return 0;
+}
+
+void model_release(bm_hip_model* m) {
+  if (!m) return;
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (void* p : {(void*)m->arena, (void*)m->conv_state, (void*)m->ssm_state, (void*)m->ctl,
+                  (void*)m->hist, (void*)m->out_tokens, (void*)m->x, (void*)m->proj,
+                  (void*)m->y, (void*)m->feat, (void*)m->logits, (void*)m->scale,
+                  (void*)m->act, (void*)m->xq, (void*)m->px, (void*)m->pproj, (void*)m->py,
+                  (void*)m->pscale, (void*)m->pact, (void*)m->pxq, (void*)m->ptok})
+    if (p) (void)hipFree(p);
+  if (m->ev0) (void)hipEventDestroy(m->ev0);
+  if (m->ev1) (void)hipEventDestroy(m->ev1);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
+  m->vocab = v.vocab;
+  m->dm = v.d_model;
+  m->nl = v.n_layers;
+  m->nh = v.n_heads;
+  m->di = 2 * v.d_model;
+  m->hd = m->di / m->nh;
+  m->pd = 2 * m->di + 3 * m->nh;
+  const int dm = m->dm, di = m->di, nh = m->nh;
+  MCHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  MCHECK(hipEventCreate(&m->ev0));
+  MCHECK(hipEventCreate(&m->ev1));
+
+  // arena layout
+  auto packed_bytes = [](const bm_bit2_tensor_t* t) {
+    return (size_t)t->rows * (size_t)((t->cols + 3) / 4);
+  };
+  size_t total = up256((size_t)m->vocab * dm * 4) + 2 * up256((size_t)dm * 4) +
+                 up256(packed_bytes(&v.tensors[v.n_tensors - 1]));
+  for (int l = 0; l < m->nl; ++l) {
+    total += up256(packed_bytes(bm_bit2_layer(&v, l, BM_L_IN_PROJ))) +
+             up256(packed_bytes(bm_bit2_layer(&v, l, BM_L_OUT_PROJ)));
+    total += up256((size_t)dm * 4) + up256((size_t)4 * di * 4) + 3 * up256((size_t)di * 4) +
+             2 * up256((size_t)nh * 4) + up256((size_t)di * 4);
+  }
+  total += up256((size_t)nh * 4);  // A_log staging
+  MCHECK(hipMalloc(&m->arena, total));
+  m->arena_bytes = total;
+  uint8_t* cur = (uint8_t*)m->arena;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = cur;
+    cur += up256(bytes);
+    return p;
+  };
+  auto put_f = [&](const bm_bit2_tensor_t* t, size_t count) -> float* {
+    float* d = (float*)take(count * 4);
+    if (hipMemcpy(d, t->data, count * 4, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    return d;
+  };
+  auto put_w = [&](const bm_bit2_tensor_t* t) -> uint8_t* {
+    const size_t b = packed_bytes(t);
+    uint8_t* d = take(b);
+    if (hipMemcpy(d, t->packed, b, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    if (bm::launch_canonicalize(d, b, m->stream) != hipSuccess) return nullptr;
+    return d;
+  };
+  m->embed = put_f(&v.tensors[0], (size_t)m->vocab * dm);
+  const bm_bit2_tensor_t* fin = &v.tensors[1 + BM_L_COUNT * m->nl];
+  m->norm_f = put_f(&fin[0], dm);
+  m->lm_norm = put_f(&fin[1], dm);
+  m->lm_head = put_w(&fin[2]);
+  m->lm_scale = fin[2].scale;
+  if (!m->embed || !m->norm_f || !m->lm_norm || !m->lm_head) {
+    bm_set_error("upload failed");
+    return -1;
+  }
+  float* alog = (float*)take((size_t)nh * 4);
+  std::vector<float> wt((size_t)4 * di);
+  m->L.resize(m->nl);
+  for (int l = 0; l < m->nl; ++l) {
+    Layer& Ly = m->L[l];
+    const bm_bit2_tensor_t* t = bm_bit2_layer(&v, l, 0);
+    Ly.in_norm = put_f(&t[BM_L_IN_NORM], dm);
+    Ly.in_proj = put_w(&t[BM_L_IN_PROJ]);
+    Ly.in_scale = t[BM_L_IN_PROJ].scale;
+    // conv1d weight [channel][tap] -> [tap][channel] (src/model.c:794-805)
+    for (int tap = 0; tap < 4; ++tap)
+      for (int ch = 0; ch < di; ++ch) {
+        float w;
+        memcpy(&w, (const uint8_t*)t[BM_L_CONV_W].data + ((size_t)ch * 4 + tap) * 4, 4);
+        wt[(size_t)tap * di + ch] = w;
+      }
+    Ly.conv_wt = (float*)take((size_t)4 * di * 4);
+    MCHECK(hipMemcpy(Ly.conv_wt, wt.data(), (size_t)4 * di * 4, hipMemcpyHostToDevice));
+    Ly.conv_b = put_f(&t[BM_L_CONV_B], di);
+    Ly.dt_bias = put_f(&t[BM_L_DT_BIAS], nh);
+    MCHECK(hipMemcpy(alog, t[BM_L_A_LOG].data, (size_t)nh * 4, hipMemcpyHostToDevice));
+    Ly.A = (float*)take((size_t)nh * 4);
+    hipLaunchKernelGGL(bm::k_neg_exp, dim3((nh + 255) / 256), dim3(256), 0, m->stream, alog,
+                       Ly.A, nh);
+    MCHECK(hipGetLastError());
+    MCHECK(hipStreamSynchronize(m->stream));
+    Ly.D = put_f(&t[BM_L_D], di);
+    Ly.out_norm = put_f(&t[BM_L_OUT_NORM], di);
+    Ly.out_proj = put_w(&t[BM_L_OUT_PROJ]);
+    Ly.out_scale = t[BM_L_OUT_PROJ].scale;
+    if (!Ly.in_norm || !Ly.in_proj || !Ly.conv_b || !Ly.dt_bias || !Ly.D || !Ly.out_norm ||
+        !Ly.out_proj) {
+      bm_set_error("upload failed");
+      return -1;
+    }
+  }
+  // state + scratch
+  MCHECK(hipMalloc(&m->conv_state, (size_t)m->nl * 3 * di * 4));
+  MCHECK(hipMalloc(&m->ssm_state, (size_t)m->nl * di * 4));
+  MCHECK(hipMemset(m->conv_state, 0, (size_t)m->nl * 3 * di * 4));
+  MCHECK(hipMemset(m->ssm_state, 0, (size_t)m->nl * di * 4));
+  MCHECK(hipMalloc(&m->ctl, bm::CTL_WORDS * 4));
+  MCHECK(hipMemset(m->ctl, 0, bm::CTL_WORDS * 4));
+  MCHECK(hipMalloc(&m->hist, bm::kHistory * 4));
+  MCHECK(hipMemset(m->hist, 0, bm::kHistory * 4));
+  MCHECK(hipMalloc(&m->x, (size_t)dm * 4));
+  MCHECK(hipMalloc(&m->proj, (size_t)m->pd * 4));
+  MCHECK(hipMalloc(&m->y, (size_t)di * 4));
+  MCHECK(hipMalloc(&m->feat, (size_t)dm * 4));
+  MCHECK(hipMalloc(&m->logits, (size_t)m->vocab * 4));
+  MCHECK(hipMalloc(&m->scale, 64));
+  MCHECK(hipMalloc(&m->act, bm::act_row_bytes(di > dm ? di : dm)));
+  MCHECK(hipMalloc(&m->xq, (size_t)(di > dm ? di : dm)));
+  MCHECK(hipDeviceSynchronize());
+  return 0;
+}
+
+int set_ctl(bm_hip_model* m, int token, const int* history, int history_len) {
+  int h[bm::kHistory];
+  const int len = history_len < bm::kHistory ? history_len : bm::kHistory;
+  for (int j = 0; j < len; ++j) h[j] = history[history_len - len + j];
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipMemcpyAsync(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  ctl[bm::CTL_TOKEN] = token;
+  ctl[bm::CTL_STEP] = 0;
+  ctl[bm::CTL_HCOUNT] = len;
+  MCHECK(hipMemcpyAsync(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice, m->stream));
+  if (len) MCHECK(hipMemcpyAsync(m->hist, h, (size_t)len * 4, hipMemcpyHostToDevice, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  return 0;
+}
+
+int ensure_out(bm_hip_model* m, int n) {
+  if (n <= m->out_cap) return 0;
+  if (m->out_tokens) (void)hipFree(m->out_tokens);
+  m->out_tokens = nullptr;
+  m->out_cap = 0;
+  if (m->exec) {  // the captured graph refers to the old buffer
+    (void)hipGraphExecDestroy(m->exec);
+    (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+  }
+  MCHECK(hipMalloc(&m->out_tokens, (size_t)n * 4));
+  m->out_cap = n;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" bm_hip_model_t* bm_hip_model_load(const void* image, size_t size) {
+  if (!bm_hip_init()) return nullptr;
+  bm_bit2_view_t v;
+  const int rc = bm_bit2_parse(image, size, &v);
+  if (rc != 0) {
+    bm_set_error(rc == -1 ? "malformed BIT2 image" : "BIT2 shapes rejected by the loader");
+    return nullptr;
+  }
+  bm_hip_model* m = new bm_hip_model();
+  const int ok = load_into(m, v);
+  bm_bit2_view_free(&v);
+  if (ok != 0) {
+    model_release(m);
+    return nullptr;
+  }
+  return m;
+}
+
+extern "C" void bm_hip_model_free(bm_hip_model_t* m) { model_release(m); }
+
+extern "C" int bm_hip_model_config(const bm_hip_model_t* m, int which) {
+  switch (which) {
+    case 0: return m->vocab;
+    case 1: return m->dm;
+    case 2: return m->nl;
+    case 3: return m->nh;
+    default: return m->di;
+  }
+}
+
+extern "C" int bm_hip_model_reset(bm_hip_model_t* m) {
+  MCHECK(hipMemsetAsync(m->conv_state, 0, (size_t)m->nl * 3 * m->di * 4, m->stream));
+  MCHECK(hipMemsetAsync(m->ssm_state, 0, (size_t)m->nl * m->di * 4, m->stream));
+  MCHECK(hipMemsetAsync(m->ctl, 0, bm::CTL_WORDS * 4, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  return 0;
+}
+
+extern "C" int bm_hip_model_prefill(bm_hip_model_t* m, const int32_t* tokens, int n) {
+  if (n <= 0) return 0;
+  if (ensure_prefill(m, n)) return -1;
+  hipStream_t s = m->stream;
+  const int dm = m->dm, di = m->di;
+  MCHECK(hipMemcpyAsync(m->ptok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
+  hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, n), dim3(256), 0, s, m->embed, dm,
+                     m->vocab, m->ptok, m->px);
+  MCHECK(hipGetLastError());
+  for (int l = 0; l < m->nl; ++l) {
+    const Layer& Ly = m->L[l];
+    // block_step_batch (src/block.c:378-447): batched in_proj, token-serial
+    // SSM, batched out_proj, then x += out (src/model.c:1139-1142)
+    if (bitlinear(m, m->px, n, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->pproj,
+                  bm::MODE_STORE, m->pact, m->pscale, m->pxq, s))
+      return -1;
+    hipLaunchKernelGGL(bm::k_ssm_batch, dim3((di + 255) / 256), dim3(256), 0, s, m->pproj, m->pd,
+                       n, di, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b,
+                       m->conv_state + (size_t)l * 3 * di, m->ssm_state + (size_t)l * di, Ly.D,
+                       m->py, m->ctl);
+    MCHECK(hipGetLastError());
+    if (bitlinear(m, m->py, n, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->px,
+                  bm::MODE_ACC, m->pact, m->pscale, m->pxq, s))
+      return -1;
+  }
+  hipLaunchKernelGGL(bm::k_advance_pos, dim3(1), dim3(64), 0, s, m->ctl, n);
+  MCHECK(hipGetLastError());
+  MCHECK(hipStreamSynchronize(s));
+  return 0;
+}
+
+extern "C" int bm_hip_model_step(bm_hip_model_t* m, int token, const int* history,
+                                 int history_len, float penalty) {
+  if (token < 0 || token >= m->vocab) return 0;  // src/model.c:1188-1193
+  if (set_ctl(m, token, history, history_len)) return -1;
+  if (enqueue_step(m, m->stream, penalty, false)) return -1;
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipMemcpyAsync(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  return ctl[bm::CTL_TOKEN];
+}
+
+extern "C" int bm_hip_model_logits(const bm_hip_model_t* m, float* out) {
+  MCHECK(hipMemcpyAsync(out, m->logits, (size_t)m->vocab * 4, hipMemcpyDeviceToHost, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  return 0;
+}
+
+extern "C" int bm_hip_model_layer_state(const bm_hip_model_t* m, int layer, float* conv_state,
+                                        float* ssm_state) {
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipMemcpy(conv_state, m->conv_state + (size_t)layer * 3 * m->di, (size_t)3 * m->di * 4,
+                   hipMemcpyDeviceToHost));
+  MCHECK(hipMemcpy(ssm_state, m->ssm_state + (size_t)layer * m->di, (size_t)m->di * 4,
+                   hipMemcpyDeviceToHost));
+  MCHECK(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
+  return ctl[bm::CTL_POS];
+}
+
+extern "C" int bm_hip_model_generate(bm_hip_model_t* m, const int32_t* prompt, int n_prompt,
+                                     int n_steps, float penalty, int stop_on_eos,
+                                     int32_t* out_tokens, double* decode_ms) {
+  if (n_prompt <= 0 || n_steps < 0) {
+    bm_set_error("generate: empty prompt");
+    return -1;
+  }
+  // src/main.c:451-500: prefill all but the last prompt token, history =
+  // the prompt, then greedy steps from the last prompt token
+  if (n_prompt > 1 && bm_hip_model_prefill(m, prompt, n_prompt - 1)) return -1;
+  if (set_ctl(m, prompt[n_prompt - 1], prompt, n_prompt)) return -1;
+  if (ensure_out(m, n_steps > 0 ? n_steps : 1)) return -1;
+  if (ensure_graph(m, penalty, true)) return -1;
+  MCHECK(hipEventRecord(m->ev0, m->stream));
+  for (int i = 0; i < n_steps; ++i) MCHECK(hipGraphLaunch(m->exec, m->stream));
+  MCHECK(hipEventRecord(m->ev1, m->stream));
+  MCHECK(hipEventSynchronize(m->ev1));
+  float ms = 0.0f;
+  MCHECK(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  if (decode_ms) *decode_ms = ms;
+  MCHECK(hipMemcpy(out_tokens, m->out_tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
+  int n = n_steps;
+  if (stop_on_eos)
+    for (int i = 0; i < n_steps; ++i)
+      if (out_tokens[i] == 50256 || out_tokens[i] == 0) {
+        n = i + 1;
+        break;
+      }
+  return n;
+}
+
+extern "C" int bm_hip_model_decode(bm_hip_model_t* m, int n_steps, float penalty,
+                                   double* decode_ms) {
+  // continues from the current device state (token, history, position)
+  if (ensure_out(m, n_steps > 0 ? n_steps : 1)) return -1;
+  if (ensure_graph(m, penalty, true)) return -1;
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipMemcpyAsync(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  ctl[bm::CTL_STEP] = 0;
+  MCHECK(hipMemcpyAsync(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice, m->stream));
+  MCHECK(hipEventRecord(m->ev0, m->stream));
+  for (int i = 0; i < n_steps; ++i) MCHECK(hipGraphLaunch(m->exec, m->stream));
+  MCHECK(hipEventRecord(m->ev1, m->stream));
+  MCHECK(hipEventSynchronize(m->ev1));
+  float ms = 0.0f;
+  MCHECK(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  if (decode_ms) *decode_ms = ms;
+  return 0;
+}
+
+extern "C" int bm_hip_model_tokens(const bm_hip_model_t* m, int32_t* out, int n) {
+  if (n > m->out_cap) n = m->out_cap;
+  MCHECK(hipMemcpy(out, m->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost));
+  return n;
+}
+
+// Diagnostic: evaluates the device libm restatement (fn 0 = expf, 1 = logf).
+namespace bm {
+__global__ void k_libm_eval(int fn, const float* __restrict__ in, float* __restrict__ out,
+                            size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = fn == 0 ? libm::expf_glibc(in[i]) : libm::logf_glibc(in[i]);
+}
+}  // namespace bm
+
+extern "C" int bm_hip_libm_eval_dev(int fn, const float* in, float* out, size_t n, void* stream) {
+  if (!bm_hip_init()) return -1;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(bm::k_libm_eval, dim3(blocks), dim3(256), 0, (hipStream_t)stream, fn, in,
+                     out, n);
+  MCHECK(hipGetLastError());
+  return 0;
+}

@@ -18,14 +18,6 @@
 #include "bm_hip.h"
 #include "bm_bit2.h"
 
-namespace bm {
-hipError_t launch_rms_norm(const float* x, int n, const float* gamma, float* out, float* max_out,
-                           hipStream_t s);
-bool product_needs_generic(int M, int K);
-hipError_t launch_generic(const int8_t* xq, int ldx, const float* scale_x, int M,
-                          const uint8_t* packed, int N, int K, float w_scale, float* out,
-                          int32_t* out_i32, hipStream_t s);
-}  // namespace bm
 
 static thread_local char g_err[512];
 
@@ -197,10 +189,10 @@ void host_bitlinear(const float* x, int M, int n, const uint8_t* packed, int row
   if (e == hipSuccess) {
     if (generic)
       e = bm::launch_generic((const int8_t*)b.d_q.ptr, n, (const float*)b.d_scale.ptr, M, dW,
-                             rows, cols, w_scale, (float*)b.d_out.ptr, nullptr, s);
+                             rows, cols, w_scale, b.d_out.ptr, bm::MODE_STORE, s);
     else
       e = bm::launch_product((const uint8_t*)b.d_act.ptr, (const float*)b.d_scale.ptr, M, dW,
-                             rows, cols, w_scale, true, (float*)b.d_out.ptr, nullptr, s);
+                             rows, cols, w_scale, true, b.d_out.ptr, bm::MODE_STORE, s);
   }
   if (e == hipSuccess)
     e = hipMemcpyAsync(hs, b.d_out.ptr, obytes, hipMemcpyDeviceToHost, s);
@@ -443,7 +435,8 @@ extern "C" int bm_hip_bitlinear_act_dev(const void* act, const float* scale_x, i
     return -2;
   }
   BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, scale_x, M, packed, N, K, w_scale,
-                                      canonical != 0, out, nullptr, stream_or_default(stream)),
+                                      canonical != 0, out, bm::MODE_STORE,
+                                      stream_or_default(stream)),
                    -1);
   return 0;
 }
@@ -469,11 +462,11 @@ extern "C" int bm_hip_bitlinear_dev(const float* x, int M, int K, const float* n
                    -1);
   if (generic)
     BM_HIP_CHECK_RET(bm::launch_generic(x_quant, quant_stride, scale_x, M, packed, N, K, w_scale,
-                                        out, nullptr, s),
+                                        out, bm::MODE_STORE, s),
                      -1);
   else
     BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, scale_x, M, packed, N, K, w_scale,
-                                        canonical != 0, out, nullptr, s),
+                                        canonical != 0, out, bm::MODE_STORE, s),
                      -1);
   return 0;
 }
@@ -488,7 +481,8 @@ extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
   }
   hipStream_t s = stream_or_default(stream);
   if (bm::product_needs_generic(M, K)) {
-    BM_HIP_CHECK_RET(bm::launch_generic(xq, ldx, nullptr, M, packed, N, K, 0.0f, nullptr, out, s),
+    BM_HIP_CHECK_RET(bm::launch_generic(xq, ldx, nullptr, M, packed, N, K, 0.0f, out,
+                                        bm::MODE_I32, s),
                      -1);
     return 0;
   }
@@ -498,7 +492,62 @@ extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
   }
   BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act, s), -1);
   BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, nullptr, M, packed, N, K, 0.0f,
-                                      canonical != 0, nullptr, out, s),
+                                      canonical != 0, out, bm::MODE_I32, s),
                    -1);
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Timing and calibration helpers (no reference counterpart)
+// ---------------------------------------------------------------------------
+extern "C" void* bm_hip_stream(void) {
+  if (!bm_hip_init()) return nullptr;
+  return (void*)B().stream;
+}
+
+extern "C" void* bm_hip_event_create(void) {
+  if (!bm_hip_init()) return nullptr;
+  hipEvent_t e = nullptr;
+  BM_HIP_CHECK_RET(hipEventCreate(&e), nullptr);
+  return (void*)e;
+}
+
+extern "C" void bm_hip_event_destroy(void* ev) {
+  if (ev) (void)hipEventDestroy((hipEvent_t)ev);
+}
+
+extern "C" int bm_hip_event_record(void* ev, void* stream) {
+  BM_HIP_CHECK_RET(hipEventRecord((hipEvent_t)ev, stream_or_default(stream)), -1);
+  return 0;
+}
+
+extern "C" float bm_hip_event_elapsed_ms(void* start, void* stop) {
+  float ms = -1.0f;
+  if (hipEventSynchronize((hipEvent_t)stop) != hipSuccess) return -1.0f;
+  if (hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop) != hipSuccess) return -1.0f;
+  return ms;
+}
+
+namespace bm {
+__global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+}  // namespace bm
+
+extern "C" int bm_hip_copy_dev(void* dst, const void* src, size_t bytes, void* stream) {
+  if (!bm_hip_init()) return -1;
+  if (bytes % 16 || ((uintptr_t)dst | (uintptr_t)src) % 16) {
+    bm_set_error("copy: 16-byte sizes and alignment only");
+    return -2;
+  }
+  const size_t n = bytes / 16;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(bm::k_copy16, dim3(blocks), dim3(256), 0, stream_or_default(stream),
+                     (const uint4*)src, (uint4*)dst, n);
+  BM_HIP_CHECK_RET(hipGetLastError(), -1);
   return 0;
 }

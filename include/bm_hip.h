@@ -147,6 +147,17 @@ int bm_hip_synchronize(void);
 /* Rewrites 2-bit code 11 to 10 in place (device buffer of `bytes`). */
 int bm_hip_canonicalize_dev(uint8_t *packed, size_t bytes, void *stream);
 
+/* Timing and calibration (no reference counterpart; the reference times
+ * with CLOCK_MONOTONIC, src/utils.c:90-95): HIP events on a stream (NULL =
+ * the library's stream), and a plain 16-byte copy kernel whose HBM counters
+ * calibrate traffic measurements. */
+void *bm_hip_stream(void);
+void *bm_hip_event_create(void);
+void bm_hip_event_destroy(void *ev);
+int bm_hip_event_record(void *ev, void *stream);
+float bm_hip_event_elapsed_ms(void *start, void *stop);
+int bm_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
+
 /* ------------------------------------------------------------------ */
 /* Device-pointer kernels (asynchronous on `stream`)                    */
 /* ------------------------------------------------------------------ */
@@ -216,6 +227,76 @@ int bm_hip_ternary_gemm_i32_dev(const int8_t *xq,
                                 int32_t *out,
                                 void *act,
                                 void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Device-resident model: the reference's model API (src/bitmamba.h:    */
+/* 282-294, src/model.c:477-1314) with weights, activations and the    */
+/* recurrent state in HBM.  Greedy sampling only (temp < 0.05,         */
+/* src/model.c:143-154); repetition penalty supported.                 */
+/* ------------------------------------------------------------------ */
+typedef struct bm_hip_model bm_hip_model_t;
+
+/* model_load (src/model.c:477-932) from a BIT2 image in memory: same
+ * validation; weights copied to one device arena (packed tensors with code
+ * 11 rewritten to 10), A = -expf(A_log) and the conv transpose computed at
+ * load.  NULL on failure (reason in bm_hip_last_error()). */
+bm_hip_model_t *bm_hip_model_load(const void *image, size_t size);
+/* model_free (src/model.c:1316-1372) */
+void bm_hip_model_free(bm_hip_model_t *m);
+/* 0 vocab, 1 d_model, 2 n_layers, 3 n_heads, 4 d_inner */
+int bm_hip_model_config(const bm_hip_model_t *m, int which);
+/* zero recurrent state and ring position (block_init_cache,
+ * src/block.c:11-26) */
+int bm_hip_model_reset(bm_hip_model_t *m);
+/* model_prefill (src/model.c:1045-1153): n tokens through every layer,
+ * batched BitLinear + token-serial SSM; no LM head.  0 or -1. */
+int bm_hip_model_prefill(bm_hip_model_t *m, const int32_t *tokens, int n);
+/* model_forward_step with temp < 0.05 (src/model.c:1175-1314): returns the
+ * greedy next token; history[history_len] as the reference's caller keeps
+ * it (the last 256 tokens are used). */
+int bm_hip_model_step(bm_hip_model_t *m,
+                      int token,
+                      const int *history,
+                      int history_len,
+                      float penalty);
+/* copies the logits of the last step (after the penalty) */
+int bm_hip_model_logits(const bm_hip_model_t *m, float *out);
+/* copies one layer's conv_state [3][d_inner] and ssm_state [d_inner];
+ * returns the ring position */
+int bm_hip_model_layer_state(const bm_hip_model_t *m,
+                             int layer,
+                             float *conv_state,
+                             float *ssm_state);
+/* The decode loop of src/main.c:443-500 on the device: prefill
+ * prompt[0..n-2], history = prompt, then n_steps greedy steps from
+ * prompt[n-1], each step one replay of a captured hipGraph with no host
+ * synchronization.  Writes the tokens; *decode_ms = device time of the
+ * steps (prefill excluded, as the reference's tok/s).  Returns the number of
+ * tokens (cut after the first 50256 or 0 when stop_on_eos), -1 on error. */
+int bm_hip_model_generate(bm_hip_model_t *m,
+                          const int32_t *prompt,
+                          int n_prompt,
+                          int n_steps,
+                          float penalty,
+                          int stop_on_eos,
+                          int32_t *out_tokens,
+                          double *decode_ms);
+/* n_steps more greedy steps from the current device state; tokens
+ * readable with bm_hip_model_tokens. */
+int bm_hip_model_decode(bm_hip_model_t *m,
+                        int n_steps,
+                        float penalty,
+                        double *decode_ms);
+int bm_hip_model_tokens(const bm_hip_model_t *m, int32_t *out, int n);
+
+/* Diagnostic (no reference counterpart): evaluates the device restatement of
+ * the libm functions the SSM step uses (fn 0 = expf, 1 = logf) on n device
+ * floats, for checks against the host libm. */
+int bm_hip_libm_eval_dev(int fn,
+                         const float *in,
+                         float *out,
+                         size_t n,
+                         void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Synthetic BIT2 images (counterpart: the writer scripts/export-bin.py  */

@@ -734,3 +734,18 @@ int orc_model_layer_state(const orc_model_t *m,
     memcpy(ssm_state, b->ssm_state, (size_t) m->d_inner * sizeof(float));
     return b->conv_pos;
 }
+
+/* glibc expf / logf over an array (the functions scalar_ssm_inner calls) */
+void orc_expf_array(const float *in, float *out, size_t n)
+{
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; i++)
+        out[i] = expf(in[i]);
+}
+
+void orc_logf_array(const float *in, float *out, size_t n)
+{
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; i++)
+        out[i] = logf(in[i]);
+}

@@ -146,6 +146,10 @@ int orc_model_layer_state(const orc_model_t *m,
                           float *conv_state,
                           float *ssm_state);
 
+/* libm expf / logf applied elementwise (the values the SSM step sees) */
+void orc_expf_array(const float *in, float *out, size_t n);
+void orc_logf_array(const float *in, float *out, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

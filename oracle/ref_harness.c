@@ -45,6 +45,12 @@ const char *bmref_init(int threads, int kind)
     return g_kernels.name;
 }
 
+/* pool wait policy: 0 = condvar, 100 = pure spin (the reference default) */
+void bmref_set_poll(int intensity)
+{
+    bm_set_poll(intensity);
+}
+
 void bmref_shutdown(void)
 {
     bm_thread_pool_free();

@@ -51,11 +51,14 @@ _ORACLE_SIGS = {
     "orc_model_logits": (C.POINTER(C.c_float), [_vp]),
     "orc_model_config": (_i, [_vp, _i]),
     "orc_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
+    "orc_expf_array": (None, [_vp, _vp, _sz]),
+    "orc_logf_array": (None, [_vp, _vp, _sz]),
 }
 
 _REF_SIGS = {
     "bmref_init": (C.c_char_p, [_i, _i]),
     "bmref_shutdown": (None, []),
+    "bmref_set_poll": (None, [_i]),
     "bmref_threads": (_i, []),
     "bmref_rms_norm": (_f, [_vp, _i, _vp, _vp]),
     "bmref_bitlinear_forward": (None, [_vp, _i, _vp, _i, _i, _f, _vp, _vp, _vp, _vp]),
@@ -175,3 +178,20 @@ def decode_dense(packed, cols):
     codes = np.stack([(p >> (2 * j)) & 3 for j in range(4)], axis=-1).reshape(p.shape[0], -1)
     w = np.minimum(codes.astype(np.int32) - 1, 1)
     return w[:, :cols]
+
+
+def same_bits(a, b, what="values"):
+    """Asserts bitwise equality of two arrays; on failure reports how many
+    elements differ and the first few, never a full dump."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    assert a.shape == b.shape, "%s: shape %s vs %s" % (what, a.shape, b.shape)
+    va = a.view(np.uint8).reshape(a.size, -1) if a.size else a
+    vb = b.view(np.uint8).reshape(b.size, -1) if b.size else b
+    diff = np.any(va != vb, axis=1) if a.size else np.zeros(0, bool)
+    n = int(diff.sum())
+    if n:
+        idx = np.flatnonzero(diff)[:6]
+        fa, fb = a.reshape(-1), b.reshape(-1)
+        pairs = ", ".join("[%d] %r vs %r" % (i, fa[i], fb[i]) for i in idx)
+        raise AssertionError("%s: %d of %d elements differ: %s" % (what, n, a.size, pairs))

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import native
-from native import bh, ptr
+from native import bh, ptr, same_bits
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -73,7 +73,7 @@ def test_quantize_golden(hip):
         note("quantize golden n=%d" % n)
         x, g = z["x_%d" % n], z["g_%d" % n]
         xn, xq, _ = gpu_quantize(hip, x, g, act=(n % 16 == 0))
-        assert xn.tobytes() == z["xn_%d" % n].tobytes()
+        same_bits(xn, z["xn_%d" % n], "xn")
         np.testing.assert_array_equal(xq, z["xq_%d" % n])
 
 
@@ -88,9 +88,9 @@ def test_quantize_random_vs_oracle(hip, n):
     g = (r.standard_normal(n) * 0.02).astype(np.float32)
     xn, xq, sc = gpu_quantize(hip, x, g)
     on, oq, osc, _ = native.orc_quantize_rows(x, g)
-    assert xn.tobytes() == on.tobytes()
+    same_bits(xn, on, "xn")
     np.testing.assert_array_equal(xq, oq)
-    assert sc.tobytes() == osc.tobytes()
+    same_bits(sc, osc, "sc")
 
 
 def test_rms_norm_dropin(hip):
@@ -103,7 +103,7 @@ def test_rms_norm_dropin(hip):
         mx = hip.hip_rms_norm(ptr(x), n, ptr(g), ptr(out))
         ref = np.empty(n, np.float32)
         rmx = native.oracle().orc_rms_norm(ptr(x), n, ptr(g), ptr(ref))
-        assert out.tobytes() == ref.tobytes()
+        same_bits(out, ref, "out")
         assert np.float32(mx) == np.float32(rmx)
 
 
@@ -192,7 +192,7 @@ def test_bitlinear_fp32_exact(hip, M, K, N):
     ref, _, rq = native.orc_bitlinear(x, packed, N, K, 0.02, g)
     np.testing.assert_array_equal(xq, rq)
     assert rel_err(out, ref) <= 1e-4
-    assert out.tobytes() == ref.tobytes()
+    same_bits(out, ref, "out")
 
 
 def test_prefill_shapes_sampled(hip):
@@ -212,7 +212,7 @@ def test_prefill_shapes_sampled(hip):
         rows = np.unique(np.concatenate([[0, 1, 127, 128, M - 1], r.integers(0, M, 35)]))
         ref, _, rq = native.orc_bitlinear(x[rows], packed, N, K, 0.02, g)
         np.testing.assert_array_equal(xq[rows], rq)
-        assert out[rows].tobytes() == ref.tobytes()
+        same_bits(out[rows], ref, "out[rows]")
 
 
 # ------------------------------------------------------------ drop-in ABI
@@ -228,8 +228,8 @@ def test_dropin_cfg1_golden(hip):
     xn = np.empty(K, np.float32)
     xq = np.zeros(K + 32, np.int8)
     hip.hip_bitlinear_forward(ptr(x), K, C.byref(w), C.byref(nw), ptr(out), ptr(xn), ptr(xq))
-    assert out.tobytes() == z["out"][0].tobytes()
-    assert xn.tobytes() == z["x_norm"].tobytes()
+    same_bits(out, z["out"][0], "out")
+    same_bits(xn, z["x_norm"], "xn")
     np.testing.assert_array_equal(xq[:K], z["x_quant"][0])
 
 
@@ -247,7 +247,7 @@ def test_dropin_batch_golden_shapes(hip):
         xq = np.zeros((M, K + 32), np.int8)
         hip.hip_bitlinear_forward_batch(ptr(x), M, K, C.byref(w), C.byref(nw), ptr(out),
                                         ptr(xn), ptr(xq), K + 32)
-        assert out.tobytes() == z["out_" + key].tobytes()
+        same_bits(out, z["out_" + key], "out")
         np.testing.assert_array_equal(xq[:, :K], z["xq_" + key])
 
 

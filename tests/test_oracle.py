@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import native
-from native import bh, ptr
+from native import bh, ptr, same_bits
 
 
 def rnd(seed):
@@ -66,8 +66,8 @@ def test_rms_norm_vs_reference(ref_lib, n):
         b = np.empty(n, np.float32)
         ma = O.orc_rms_norm(ptr(x), n, ptr(g), ptr(a))
         mb = ref_lib.bmref_rms_norm(ptr(x), n, ptr(g), ptr(b))
-        assert np.float32(ma).tobytes() == np.float32(mb).tobytes()
-        assert a.tobytes() == b.tobytes()
+        same_bits(np.float32(ma), np.float32(mb), "np.float32(ma)")
+        same_bits(a, b, "a")
 
 
 def test_quantize_invariants():
@@ -113,7 +113,7 @@ def test_bitlinear_vs_reference(ref_lib, K, N):
     a = native.orc_bitlinear(x, packed, N, K, 0.02, g)
     b = native.ref_bitlinear(x, packed, N, K, 0.02, g)
     for u, v in zip(a, b):
-        assert u.tobytes() == v.tobytes()
+        same_bits(u, v, "u")
 
 
 @pytest.mark.parametrize("K,N", [(1024, 50), (2048, 31), (1030, 9), (4096, 12)])
@@ -147,7 +147,7 @@ def test_rows_epilogue_order():
     acc = np.zeros(N, np.float32)
     for s in range(4):
         acc = (acc + (st[:, s].astype(np.float32) * inv).astype(np.float32)).astype(np.float32)
-    assert out.tobytes() == acc.tobytes()
+    same_bits(out, acc, "out")
 
 
 # ----------------------------------------------------------- a15 SSM step
@@ -194,7 +194,7 @@ def test_ssm_inner_vs_reference(ref_lib):
             ref_lib.bmref_ssm_inner(C.byref(a), 0, di)
         outs.append((cs_, st_, y))
     for u, v in zip(*outs):
-        assert u.tobytes() == v.tobytes()
+        same_bits(u, v, "u")
 
 
 # --------------------------------------------------- end-to-end (model)
@@ -258,7 +258,7 @@ def test_model_vs_reference(ref_lib, tmp_path, seed, dist):
     t2, l2 = _ref_stream(ref_lib, str(path), prompt, 12)
     assert t1 == t2
     for a, b in zip(l1, l2):
-        assert a.tobytes() == b.tobytes()
+        same_bits(a, b, "a")
 
 
 def test_model_loader_rejects_malformed():
