@@ -152,53 +152,90 @@ def leg_prefill(L, reps=10):
         qms = ev.stop_ms() / reps
         tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         out["%dx%dx%d" % (M, K, N)] = dict(gemm_us=round(ms * 1e3, 1), tops=round(tops, 1),
-                                           frac=round(tops * 1e3 / I8_PEAK_TOPS, 4),
+                                           frac=round(tops / I8_PEAK_TOPS, 4),
                                            quantize_us=round(qms * 1e3, 1))
         for b in (dW, dx, dg, dq, ds, da, dout):
             b.free()
     return out
 
 
-def leg_cpu(sample_tokens=48):
-    """The reference's own C (oracle/_ref: dispatch_init -> AVX2+FMA kernels,
-    its thread pool) decoding the same synthetic 1B-shape model."""
+def cpu_threads():
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    return max(1, min(allowed, 16))
+
+
+def cpu_child(threads, sample_tokens, budget_s):
+    """Runs in a separate process that never touches the GPU: the
+    reference's own C (oracle/_ref: dispatch_init -> AVX2+FMA kernels, its
+    thread pool with the default spin wait) decoding the same synthetic
+    1B-shape model.  Prints one JSON line."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import native
-    if not native.ref_available():
-        return None
     R = native.ref()
-    threads = min(os.cpu_count() or 1, 16)
     name = R.bmref_init(threads, 1).decode()
-    R.bmref_set_poll(100)                            # the reference's default wait policy
+    R.bmref_set_poll(100)
     c = CFG_1B
     blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
                           c["dist"])
     prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
-    d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    d = tempfile.gettempdir()
     with tempfile.NamedTemporaryFile(suffix=".bin", dir=d) as f:
         blob.tofile(f.name)
         del blob
+        log("cpu: model file written, loading with %d threads (%s kernels)" % (threads, name))
         h = R.bmref_model_load(f.name.encode())
         p = np.ascontiguousarray(prompt[:-1], np.int32)
+        t0 = time.perf_counter()
         R.bmref_model_prefill(h, native.ptr(p), p.size)
+        log("cpu: prefill of %d tokens %.2fs" % (p.size, time.perf_counter() - t0))
         hist = [int(t) for t in prompt]
         cur = int(prompt[-1])
         times = []
-        for _ in range(sample_tokens):
+        start = time.perf_counter()
+        for i in range(sample_tokens):
             harr = np.array(hist[-256:], np.int32)
             t0 = time.perf_counter()
             cur = R.bmref_model_step(h, cur, native.ptr(harr), harr.size, 1.0)
             times.append(time.perf_counter() - t0)
             hist.append(cur)
+            if i % 8 == 0:
+                log("cpu: step %d %.1f ms" % (i, times[-1] * 1e3))
+            if time.perf_counter() - start > budget_s:
+                break
         R.bmref_model_free(h)
     R.bmref_shutdown()
     tok_s = len(times) / sum(times)
-    return dict(value=round(tok_s, 2), unit="tok/s", cores=threads, kind="reference",
-                sample="%d greedy steps of the same 1B-shape decode after a 7-token prefill "
-                       "(reference kernels: %s, %d threads)" % (sample_tokens, name, threads))
+    print(json.dumps(dict(value=round(tok_s, 2), unit="tok/s", cores=threads, kind="reference",
+                          sample="%d greedy steps of the same 1B-shape decode after a 7-token "
+                                 "prefill (reference kernels: %s, %d threads, spin-wait pool)"
+                                 % (len(times), name, threads))), flush=True)
+
+
+def leg_cpu(sample_tokens=64, budget_s=25.0, timeout_s=240):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import native
+    import subprocess
+    if not native.ref_available():
+        return None
+    threads = cpu_threads()
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child", str(threads),
+           str(sample_tokens), str(budget_s)]
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, timeout=timeout_s, text=True)
+    except subprocess.TimeoutExpired:
+        log("cpu: baseline child exceeded %ds, no baseline reported" % timeout_s)
+        return None
+    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+    return json.loads(lines[-1]) if r.returncode == 0 and lines else None
 
 
 def main():
+    if len(sys.argv) == 5 and sys.argv[1] == "--cpu-child":
+        cpu_child(int(sys.argv[2]), int(sys.argv[3]), float(sys.argv[4]))
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)

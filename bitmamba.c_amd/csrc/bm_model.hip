@@ -24,7 +24,7 @@
 namespace bm {
 
 // control block in device memory
-enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_WORDS = 8 };
+enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_TICKET = 4, CTL_WORDS = 8 };
 constexpr int kHistory = 256;  // HISTORY_MAX (src/main.c:19)
 
 __device__ __forceinline__ float silu_ref(float x) {
@@ -38,7 +38,9 @@ __device__ __forceinline__ float softplus_ref(float x) {
   return libm::logf_glibc(__fadd_rn(1.0f, libm::expf_glibc(x)));
 }
 
-// One channel of scalar_ssm_inner (src/kernel.c:34-70) for one token.
+// One channel of scalar_ssm_inner (src/kernel.c:34-70) for one token.  proj
+// holds the in_proj outputs in the device's per-head order: head h occupies
+// [h*(2hd+3), (h+1)*(2hd+3)) as [z (hd) | x (hd) | B | C | dt].
 __device__ __forceinline__ void ssm_channel(const float* __restrict__ proj, int di, int nh, int hd,
                                             int idx, int pos, const float* __restrict__ dt_bias,
                                             const float* __restrict__ A,
@@ -46,14 +48,15 @@ __device__ __forceinline__ void ssm_channel(const float* __restrict__ proj, int 
                                             const float* __restrict__ cb,
                                             float* __restrict__ cs, float* __restrict__ ssm,
                                             const float* __restrict__ D, float* __restrict__ y) {
-  const int h = idx / hd;
+  const int h = idx / hd, c = idx - h * hd;
+  const float* __restrict__ ph = proj + (size_t)h * (2 * hd + 3);
   const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
   const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
-  const float dt_val = softplus_ref(__fadd_rn(proj[2 * di + 2 * nh + h], dt_bias[h]));
+  const float dt_val = softplus_ref(__fadd_rn(ph[2 * hd + 2], dt_bias[h]));
   const float decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
-  const float Bdt = __fmul_rn(proj[2 * di + h], dt_val);
-  const float C_val = proj[2 * di + nh + h];
-  const float xin = proj[di + idx];
+  const float Bdt = __fmul_rn(ph[2 * hd], dt_val);
+  const float C_val = ph[2 * hd + 1];
+  const float xin = ph[hd + c];
   float* c0 = cs + (size_t)pos * di;
   float conv = __fadd_rn(cb[idx], __fmul_rn(c0[idx], cw[idx]));
   conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t1 * di + idx], cw[di + idx]));
@@ -63,18 +66,7 @@ __device__ __forceinline__ void ssm_channel(const float* __restrict__ proj, int 
   const float xa = silu_ref(conv);
   const float st = __fadd_rn(__fmul_rn(ssm[idx], decay), __fmul_rn(xa, Bdt));
   ssm[idx] = st;
-  y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xa, D[idx])), silu_ref(proj[idx]));
-}
-
-__global__ void k_ssm_step(const float* __restrict__ proj, int di, int nh, int hd,
-                           const float* __restrict__ dt_bias, const float* __restrict__ A,
-                           const float* __restrict__ cw, const float* __restrict__ cb,
-                           float* __restrict__ cs, float* __restrict__ ssm,
-                           const float* __restrict__ D, float* __restrict__ y,
-                           const int* __restrict__ ctl) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= di) return;
-  ssm_channel(proj, di, nh, hd, idx, ctl[CTL_POS], dt_bias, A, cw, cb, cs, ssm, D, y);
+  y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xa, D[idx])), silu_ref(ph[c]));
 }
 
 // n tokens in order; each thread owns one channel across all tokens
@@ -184,6 +176,18 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ 
   }
 }
 
+hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
+                             float w_scale, int nh, int hd, const float* dt_bias,
+                             const float* A, const float* cw, const float* cb, float* cs,
+                             float* ssm, const float* D, float* y, const int* ctl,
+                             hipStream_t s);
+hipError_t launch_rows_fused(const float* x, int K, const float* gamma, const uint8_t* W, int N,
+                             float w_scale, float* out, bool accumulate, hipStream_t s);
+hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
+                          const uint8_t* W, int N, float w_scale, float* logits, bool argmax,
+                          int* ctl, int* hist, int* out_tokens, float* part_v, int* part_i,
+                          const float* embed, float* x_next, int blocks, hipStream_t s);
+
 }  // namespace bm
 
 // ---------------------------------------------------------------------------
@@ -215,6 +219,8 @@ struct bm_hip_model {
   int out_cap = 0;
   // decode scratch
   float *x = nullptr, *proj = nullptr, *y = nullptr, *feat = nullptr, *logits = nullptr;
+  float* part_v = nullptr;  // per-block greedy candidates of the LM head
+  int* part_i = nullptr;
   float* scale = nullptr;
   uint8_t* act = nullptr;
   int8_t* xq = nullptr;
@@ -230,6 +236,9 @@ struct bm_hip_model {
   float graph_penalty = 1.0f;
   bool graph_with_out = false;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // BM_HIP_NO_GRAPH=1: enqueue each step's kernels directly instead of
+  // replaying the captured graph (for tools that cannot trace graphs)
+  bool no_graph = false;
 };
 
 namespace {
@@ -261,45 +270,48 @@ int bitlinear(bm_hip_model* m, const float* x, int M, int K, const float* norm,
   return 0;
 }
 
-// The kernels of one decode step, enqueued on s.
+constexpr int kLmBlocks = 256;
+
+// The kernels of one decode step, enqueued on s.  m->x already holds the
+// embedding of the current token.
 int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) {
   const int dm = m->dm, di = m->di;
-  hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, 1), dim3(256), 0, s, m->embed, dm,
-                     m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
-  MCHECK(hipGetLastError());
   for (int l = 0; l < m->nl; ++l) {
     const Layer& Ly = m->L[l];
     float* cs = m->conv_state + (size_t)l * 3 * di;
     float* ss = m->ssm_state + (size_t)l * di;
-    if (bitlinear(m, m->x, 1, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
-                  bm::MODE_STORE, m->act, m->scale, m->xq, s))
-      return -1;
-    hipLaunchKernelGGL(bm::k_ssm_step, dim3((di + 255) / 256), dim3(256), 0, s, m->proj, di,
-                       m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
-                       m->ctl);
-    MCHECK(hipGetLastError());
-    if (bitlinear(m, m->y, 1, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x,
-                  bm::MODE_ACC, m->act, m->scale, m->xq, s))
-      return -1;
+    // block_step, unfused branch (src/block.c:361-371) + residual
+    MCHECK(bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
+                                 Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
+                                 m->ctl, s));
+    MCHECK(bm::launch_rows_fused(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x,
+                                 true, s));
   }
-  // final RMSNorm (src/model.c:1225), then the LM head BitLinear with its own
-  // norm (src/model.c:1259-1261)
-  MCHECK(bm::launch_rms_norm(m->x, dm, m->norm_f, m->feat, nullptr, s));
-  if (bitlinear(m, m->feat, 1, dm, m->lm_norm, m->lm_head, m->vocab, m->lm_scale, m->logits,
-                bm::MODE_STORE, m->act, m->scale, m->xq, s))
-    return -1;
-  if (penalty != 1.0f) {
+  const bool fused_pick = penalty == 1.0f;  // x / 1.0f == x * 1.0f == x
+  MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab, m->lm_scale,
+                            m->logits, fused_pick, m->ctl, m->hist,
+                            write_out ? m->out_tokens : nullptr, m->part_v, m->part_i, m->embed,
+                            m->x, kLmBlocks, s));
+  if (!fused_pick) {
     hipLaunchKernelGGL(bm::k_penalty, dim3(1), dim3(bm::kHistory), 0, s, m->logits, m->vocab,
                        m->hist, m->ctl, penalty);
     MCHECK(hipGetLastError());
+    hipLaunchKernelGGL(bm::k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, m->vocab, m->ctl,
+                       m->hist, write_out ? m->out_tokens : nullptr);
+    MCHECK(hipGetLastError());
+    hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, 1), dim3(256), 0, s, m->embed, dm,
+                       m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
+    MCHECK(hipGetLastError());
   }
-  hipLaunchKernelGGL(bm::k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, m->vocab, m->ctl,
-                     m->hist, write_out ? m->out_tokens : nullptr);
-  MCHECK(hipGetLastError());
   return 0;
 }
 
 int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
+  if (m->no_graph) {
+    m->graph_penalty = penalty;
+    m->graph_with_out = write_out;
+    return 0;
+  }
   if (m->exec && m->graph_penalty == penalty && m->graph_with_out == write_out) return 0;
   if (m->exec) {
     (void)hipGraphExecDestroy(m->exec);
@@ -350,6 +362,7 @@ void model_release(bm_hip_model* m) {
   for (void* p : {(void*)m->arena, (void*)m->conv_state, (void*)m->ssm_state, (void*)m->ctl,
                   (void*)m->hist, (void*)m->out_tokens, (void*)m->x, (void*)m->proj,
                   (void*)m->y, (void*)m->feat, (void*)m->logits, (void*)m->scale,
+                  (void*)m->part_v, (void*)m->part_i,
                   (void*)m->act, (void*)m->xq, (void*)m->px, (void*)m->pproj, (void*)m->py,
                   (void*)m->pscale, (void*)m->pact, (void*)m->pxq, (void*)m->ptok})
     if (p) (void)hipFree(p);
@@ -369,6 +382,8 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
   m->pd = 2 * m->di + 3 * m->nh;
   const int dm = m->dm, di = m->di, nh = m->nh;
   MCHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  const char* ng = getenv("BM_HIP_NO_GRAPH");
+  m->no_graph = ng && ng[0] == '1';
   MCHECK(hipEventCreate(&m->ev0));
   MCHECK(hipEventCreate(&m->ev1));
 
@@ -405,6 +420,27 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
     if (bm::launch_canonicalize(d, b, m->stream) != hipSuccess) return nullptr;
     return d;
   };
+  // in_proj rows regrouped per head: [z_h | x_h | B_h | C_h | dt_h] (the
+  // reference's order is [z | x | B | C | dt], src/block.c:54-58)
+  std::vector<uint8_t> perm;
+  auto put_w_heads = [&](const bm_bit2_tensor_t* t) -> uint8_t* {
+    const size_t rb = (size_t)((t->cols + 3) / 4);
+    perm.resize((size_t)t->rows * rb);
+    const int hd = m->hd, rows_h = 2 * hd + 3;
+    for (int h = 0; h < nh; ++h) {
+      uint8_t* dst = perm.data() + (size_t)h * rows_h * rb;
+      memcpy(dst, t->packed + (size_t)h * hd * rb, hd * rb);
+      memcpy(dst + hd * rb, t->packed + (size_t)(di + h * hd) * rb, hd * rb);
+      memcpy(dst + 2 * hd * rb, t->packed + (size_t)(2 * di + h) * rb, rb);
+      memcpy(dst + (2 * hd + 1) * rb, t->packed + (size_t)(2 * di + nh + h) * rb, rb);
+      memcpy(dst + (2 * hd + 2) * rb, t->packed + (size_t)(2 * di + 2 * nh + h) * rb, rb);
+    }
+    uint8_t* d = take(perm.size());
+    if (hipMemcpy(d, perm.data(), perm.size(), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    if (bm::launch_canonicalize(d, perm.size(), m->stream) != hipSuccess) return nullptr;
+    if (hipStreamSynchronize(m->stream) != hipSuccess) return nullptr;
+    return d;
+  };
   m->embed = put_f(&v.tensors[0], (size_t)m->vocab * dm);
   const bm_bit2_tensor_t* fin = &v.tensors[1 + BM_L_COUNT * m->nl];
   m->norm_f = put_f(&fin[0], dm);
@@ -422,7 +458,7 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
     Layer& Ly = m->L[l];
     const bm_bit2_tensor_t* t = bm_bit2_layer(&v, l, 0);
     Ly.in_norm = put_f(&t[BM_L_IN_NORM], dm);
-    Ly.in_proj = put_w(&t[BM_L_IN_PROJ]);
+    Ly.in_proj = put_w_heads(&t[BM_L_IN_PROJ]);
     Ly.in_scale = t[BM_L_IN_PROJ].scale;
     // conv1d weight [channel][tap] -> [tap][channel] (src/model.c:794-805)
     for (int tap = 0; tap < 4; ++tap)
@@ -465,6 +501,8 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
   MCHECK(hipMalloc(&m->y, (size_t)di * 4));
   MCHECK(hipMalloc(&m->feat, (size_t)dm * 4));
   MCHECK(hipMalloc(&m->logits, (size_t)m->vocab * 4));
+  MCHECK(hipMalloc(&m->part_v, kLmBlocks * 4));
+  MCHECK(hipMalloc(&m->part_i, kLmBlocks * 4));
   MCHECK(hipMalloc(&m->scale, 64));
   MCHECK(hipMalloc(&m->act, bm::act_row_bytes(di > dm ? di : dm)));
   MCHECK(hipMalloc(&m->xq, (size_t)(di > dm ? di : dm)));
@@ -484,6 +522,9 @@ int set_ctl(bm_hip_model* m, int token, const int* history, int history_len) {
   ctl[bm::CTL_HCOUNT] = len;
   MCHECK(hipMemcpyAsync(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice, m->stream));
   if (len) MCHECK(hipMemcpyAsync(m->hist, h, (size_t)len * 4, hipMemcpyHostToDevice, m->stream));
+  hipLaunchKernelGGL(bm::k_embed, dim3((m->dm + 255) / 256, 1), dim3(256), 0, m->stream,
+                     m->embed, m->dm, m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
+  MCHECK(hipGetLastError());
   MCHECK(hipStreamSynchronize(m->stream));
   return 0;
 }
@@ -501,6 +542,24 @@ int ensure_out(bm_hip_model* m, int n) {
   }
   MCHECK(hipMalloc(&m->out_tokens, (size_t)n * 4));
   m->out_cap = n;
+  return 0;
+}
+
+// n_steps decode steps back to back on the model stream, timed with events
+int run_steps(bm_hip_model* m, int n_steps, double* decode_ms) {
+  MCHECK(hipEventRecord(m->ev0, m->stream));
+  for (int i = 0; i < n_steps; ++i) {
+    if (m->no_graph) {
+      if (enqueue_step(m, m->stream, m->graph_penalty, m->graph_with_out)) return -1;
+    } else {
+      MCHECK(hipGraphLaunch(m->exec, m->stream));
+    }
+  }
+  MCHECK(hipEventRecord(m->ev1, m->stream));
+  MCHECK(hipEventSynchronize(m->ev1));
+  float ms = 0.0f;
+  MCHECK(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  if (decode_ms) *decode_ms = ms;
   return 0;
 }
 
@@ -616,13 +675,7 @@ extern "C" int bm_hip_model_generate(bm_hip_model_t* m, const int32_t* prompt, i
   if (set_ctl(m, prompt[n_prompt - 1], prompt, n_prompt)) return -1;
   if (ensure_out(m, n_steps > 0 ? n_steps : 1)) return -1;
   if (ensure_graph(m, penalty, true)) return -1;
-  MCHECK(hipEventRecord(m->ev0, m->stream));
-  for (int i = 0; i < n_steps; ++i) MCHECK(hipGraphLaunch(m->exec, m->stream));
-  MCHECK(hipEventRecord(m->ev1, m->stream));
-  MCHECK(hipEventSynchronize(m->ev1));
-  float ms = 0.0f;
-  MCHECK(hipEventElapsedTime(&ms, m->ev0, m->ev1));
-  if (decode_ms) *decode_ms = ms;
+  if (run_steps(m, n_steps, decode_ms)) return -1;
   MCHECK(hipMemcpy(out_tokens, m->out_tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
   int n = n_steps;
   if (stop_on_eos)
@@ -644,14 +697,7 @@ extern "C" int bm_hip_model_decode(bm_hip_model_t* m, int n_steps, float penalty
   MCHECK(hipStreamSynchronize(m->stream));
   ctl[bm::CTL_STEP] = 0;
   MCHECK(hipMemcpyAsync(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice, m->stream));
-  MCHECK(hipEventRecord(m->ev0, m->stream));
-  for (int i = 0; i < n_steps; ++i) MCHECK(hipGraphLaunch(m->exec, m->stream));
-  MCHECK(hipEventRecord(m->ev1, m->stream));
-  MCHECK(hipEventSynchronize(m->ev1));
-  float ms = 0.0f;
-  MCHECK(hipEventElapsedTime(&ms, m->ev0, m->ev1));
-  if (decode_ms) *decode_ms = ms;
-  return 0;
+  return run_steps(m, n_steps, decode_ms);
 }
 
 extern "C" int bm_hip_model_tokens(const bm_hip_model_t* m, int32_t* out, int n) {
