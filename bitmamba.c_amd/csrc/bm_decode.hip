@@ -1,27 +1,30 @@
 // Fused single-token decode kernels (bs = 1).
 //
-// A decoded token runs 2 kernels per layer plus one for the LM head:
-//   k_inproj_ssm   one block per SSM head: quantize x (block prologue),
-//                  GEMV over the head's 2*hd+3 in_proj rows (stored
-//                  contiguously on the device), then the head's SSM step
-//                  (src/kernel.c:34-70) straight from LDS; writes y.
-//   k_rows_fused   quantize the input (block prologue), GEMV over a slice of
-//                  rows; used for out_proj with the residual add fused
-//                  (src/model.c:1214-1215) and for the LM head with the final
-//                  RMSNorm in front (src/model.c:1225, 1259-1261) and the
-//                  greedy pick at the end (src/model.c:143-154): the last
-//                  block to finish reduces the per-block maxima.
-// Every block recomputes the RMSNorm/absmax prologue of its input; the
-// sequential sum of squares (four chains, src/kernel.c:77-89) is the
-// critical path, so its LDS reads are software-pipelined 32 deep and the
-// block's first weight loads are issued before it.
+// A decoded token runs, per layer,
+//   k_rows_fused  in_proj: quantize x (block prologue) + GEMV over the
+//                 layer's in_proj rows, stored on the device per head as
+//                 [z (hd) | x (hd) | B | C | dt]
+//   k_ssm_heads   the SSM step of every channel (src/kernel.c:34-70)
+//   k_rows_fused  out_proj: quantize y + GEMV, residual add fused into the
+//                 store (src/model.c:1214-1215)
+// then the LM head (k_rows_fused with the final RMSNorm in front,
+// src/model.c:1225, 1259-1261, and a per-block greedy candidate) and
+// k_pick, which finishes the greedy choice (src/model.c:143-154), advances
+// the step state and writes the next token's embedding.
+//
+// Every block recomputes the RMSNorm/int8 prologue of its input.  Its
+// critical path is the sequential sum of squares (four fp32 chains,
+// src/kernel.c:77-89): the chains run from registers of one wave, one
+// dependent add per element, while the block's weight rows are already in
+// flight.  All elementwise prologue work runs on register-resident copies of
+// the input.  Kernel boundaries order the phases; no grid-wide fences.
 #include "bm_dev.h"
 #include "bm_libm.h"
 
 namespace bm {
 
 // control words shared with bm_model.hip
-enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_TICKET = 4 };
+enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3 };
 constexpr int kHist = 256;
 
 __device__ __forceinline__ float silu_r(float x) {
@@ -33,112 +36,210 @@ __device__ __forceinline__ float softplus_r(float x) {
   return libm::logf_glibc(__fadd_rn(1.0f, libm::expf_glibc(x)));
 }
 
-// Sequential fp32 sum of c[0..len) (one lane), loads pipelined 32 ahead.
+// ---------------------------------------------------------------------------
+// Sum of squares: four sequential chains
+// ---------------------------------------------------------------------------
+
+// chains held in registers (K/64 = E in {16, 32, 64}): lanes 16j..16j+15 of
+// wave 0 own chain j in segments of E consecutive elements; each lane adds
+// its segment to the running sum, which then moves one lane up the 16-lane
+// row (DPP row_shr:1).  After 16 rounds lane 16j+15 holds chain j's sum.
+__host__ __device__ inline bool chain_in_regs(int K) { return K == 1024 || K == 2048 || K == 4096; }
+__host__ __device__ inline int sq_stride_of(int K) { return K / 4 + 68; }
+
+template <int E>
+__device__ __forceinline__ float chain_regs(const float* __restrict__ sq, int stride, int lane) {
+  const int j = lane >> 4, seg = lane & 15;
+  const float* __restrict__ src = sq + j * stride + seg * (E + 4);
+  float v[E];
+#pragma unroll
+  for (int u = 0; u < E / 4; ++u) {
+    const float4 t = *(const float4*)(src + 4 * u);
+    v[4 * u] = t.x;
+    v[4 * u + 1] = t.y;
+    v[4 * u + 2] = t.z;
+    v[4 * u + 3] = t.w;
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+#pragma unroll
+    for (int k = 0; k < E; ++k) s = __fadd_rn(s, v[k]);
+    if (r < 15)
+      s = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(s), __float_as_int(s), 0x111,
+                                                     0xf, 0xf, false));
+  }
+  return s;
+}
+
+// other K: one lane per chain over LDS, two 32-value buffers alternating
+__device__ __forceinline__ void add32(float& s, const float4 (&b)[8]) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    s = __fadd_rn(s, b[u].x);
+    s = __fadd_rn(s, b[u].y);
+    s = __fadd_rn(s, b[u].z);
+    s = __fadd_rn(s, b[u].w);
+  }
+}
+
+__device__ __forceinline__ void load32(float4 (&b)[8], const float* __restrict__ c) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) b[u] = *(const float4*)(c + 4 * u);
+}
+
 __device__ __forceinline__ float chain_lds(const float* __restrict__ c, int len) {
   float s = 0.0f;
   int i = 0;
-  if (len >= 32) {
-    float4 cur[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) cur[u] = *(const float4*)(c + 4 * u);
-    for (; i + 32 <= len; i += 32) {
-      float4 nxt[8];
-      const bool more = i + 64 <= len;
-      if (more) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) nxt[u] = *(const float4*)(c + i + 32 + 4 * u);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        s = __fadd_rn(s, cur[u].x);
-        s = __fadd_rn(s, cur[u].y);
-        s = __fadd_rn(s, cur[u].z);
-        s = __fadd_rn(s, cur[u].w);
-      }
-      if (more) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
-      }
+  if (len >= 64) {
+    float4 A[8], B[8];
+    load32(A, c);
+    for (; i + 64 <= len; i += 64) {
+      load32(B, c + i + 32);
+      add32(s, A);
+      if (i + 96 <= len) load32(A, c + i + 64);
+      add32(s, B);
     }
   }
   for (; i < len; ++i) s = __fadd_rn(s, c[i]);
   return s;
 }
 
-// LDS layout of the quantization prologue for an input of K columns
-struct Prologue {
-  float* xs;        // [K]   input, then (PRENORM) the normalized feature
-  float* sq;        // [4][K/4 + 4]  squares, chain-major
-  uint32_t* nib;    // [K/4] split-nibble activations (4 dwords per 16 cols)
-  int* slices;      // [S]   sum of int8 values per 1024-column slice
-  float* bc;        // [8]   broadcast words
-  int sq_stride;
+// ---------------------------------------------------------------------------
+// Block prologue on register-resident input
+//   thread t owns float4 chunks c = t + i*blockDim.x (i < C), i.e. columns
+//   4c..4c+3; K % 64 == 0
+// ---------------------------------------------------------------------------
+template <int C>
+__device__ __forceinline__ void stage_load(float4 (&st)[C], const float* __restrict__ src, int K) {
+  const int n4 = K >> 2;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = threadIdx.x + i * blockDim.x;
+    st[i] = c < n4 ? ((const float4*)src)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+struct Lds {
+  float* sq;      // [4][stride] squares, chain-major (padded per segment)
+  uint32_t* nib;  // [K/4] split-nibble activations
+  int8_t* q8;     // [K] int8 activations
+  int* slices;    // [S] sum of int8 per 1024-column slice
+  float* bc;      // [32] broadcast words
+  int stride;
 };
 
-__host__ __device__ inline size_t prologue_lds_bytes(int K) {
-  const size_t sqs = (size_t)(K / 4 + 4);
-  return 4 * (size_t)K + 16 * sqs + (size_t)K + 4 * (size_t)((K + 1023) / 1024) + 64 + 64;
+__host__ __device__ inline size_t lds_bytes(int K) {
+  return 16 * (size_t)sq_stride_of(K) + 2 * (size_t)K + 4 * (size_t)((K + 1023) / 1024) + 16 + 128;
 }
 
-__device__ __forceinline__ Prologue prologue_carve(uint8_t* lds, int K) {
-  Prologue p;
-  p.sq_stride = K / 4 + 4;
-  p.sq = (float*)lds;
-  p.xs = p.sq + 4 * p.sq_stride;
-  p.nib = (uint32_t*)(p.xs + K);
-  p.slices = (int*)(p.nib + K / 4);
-  p.bc = (float*)(p.slices + (K + 1023) / 1024 + 4);
-  return p;
+__device__ __forceinline__ Lds lds_carve(uint8_t* base, int K) {
+  Lds l;
+  l.stride = sq_stride_of(K);
+  l.sq = (float*)base;
+  l.nib = (uint32_t*)(l.sq + 4 * l.stride);
+  l.q8 = (int8_t*)(l.nib + K / 4);
+  l.slices = (int*)(l.q8 + K);
+  l.bc = (float*)(l.slices + (K + 1023) / 1024 + 4);
+  return l;
 }
 
-// sum of squares of p.xs via the four chains -> rms (src/kernel.c:77-91)
-__device__ __forceinline__ float prologue_rms(const Prologue& p, int K) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  for (int i = tid; i < K; i += nt) {
-    const float v = p.xs[i];
-    p.sq[(i & 3) * p.sq_stride + (i >> 2)] = __fmul_rn(v, v);
+// rms = 1/sqrtf(sum_sq/K + 1e-6f) with the sequential four-chain sum
+// (src/kernel.c:77-91)
+template <int C>
+__device__ float pro_rms(const float4 (&xv)[C], int K, const Lds& l) {
+  const int tid = threadIdx.x, nt = blockDim.x, n4 = K >> 2;
+  const bool regs = chain_in_regs(K);
+  const int E = K >> 6;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = tid + i * nt;
+    if (c < n4) {
+      const int e = c + (regs ? 4 * (c / E) : 0);
+      l.sq[e] = __fmul_rn(xv[i].x, xv[i].x);
+      l.sq[l.stride + e] = __fmul_rn(xv[i].y, xv[i].y);
+      l.sq[2 * l.stride + e] = __fmul_rn(xv[i].z, xv[i].z);
+      l.sq[3 * l.stride + e] = __fmul_rn(xv[i].w, xv[i].w);
+    }
   }
   __syncthreads();
-  if (tid < 4) p.bc[1 + tid] = chain_lds(p.sq + tid * p.sq_stride, K >> 2);
-  __syncthreads();
-  if (tid == 0) {
-    float sum = __fadd_rn(__fadd_rn(__fadd_rn(p.bc[1], p.bc[2]), p.bc[3]), p.bc[4]);
-    p.bc[0] = cr_divf(1.0f, cr_sqrtf(__fadd_rn(cr_divf(sum, (float)K), 1e-6f)));
+  if (tid < 64) {
+    float cs = 0.0f;
+    if (regs) {
+      if (K == 1024)
+        cs = chain_regs<16>(l.sq, l.stride, tid);
+      else if (K == 2048)
+        cs = chain_regs<32>(l.sq, l.stride, tid);
+      else
+        cs = chain_regs<64>(l.sq, l.stride, tid);
+    } else if ((tid & 15) == 15) {
+      cs = chain_lds(l.sq + (tid >> 4) * l.stride, n4);
+    }
+    // lanes 15, 31, 47, 63 hold the chain sums: ((s0+s1)+s2)+s3
+    const float s0 = __shfl(cs, 15, 64), s1 = __shfl(cs, 31, 64);
+    const float s2 = __shfl(cs, 47, 64), s3 = __shfl(cs, 63, 64);
+    if (tid == 0) {
+      const float sum = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+      l.bc[0] = cr_divf(1.0f, cr_sqrtf(__fadd_rn(cr_divf(sum, (float)K), 1e-6f)));
+    }
   }
   __syncthreads();
-  return p.bc[0];
+  return l.bc[0];
 }
 
-// Quantization prologue of scalar_bitlinear_forward (src/kernel.c:356-391)
-// over an input already in p.xs; fills p.nib and p.slices, returns scale_x.
-// K % 64 == 0, blockDim.x a multiple of 64.
-__device__ float prologue_quant(const Prologue& p, int K, const float* __restrict__ gamma,
-                                float rms) {
-  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ float4 scale4(const float4& x, float rms, const float4& g) {
+  return make_float4(__fmul_rn(__fmul_rn(x.x, rms), g.x), __fmul_rn(__fmul_rn(x.y, rms), g.y),
+                     __fmul_rn(__fmul_rn(x.z, rms), g.z), __fmul_rn(__fmul_rn(x.w, rms), g.w));
+}
+
+__device__ __forceinline__ uint32_t q8_of(float v, float scale_x) {
+  const float t = __fmul_rn(v, scale_x);
+  int iv = (int)__fadd_rn(t, t >= 0.0f ? 0.5f : -0.5f);
+  iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+  return (uint32_t)(iv & 255);
+}
+
+// int8 quantization of (x*rms)*gamma (src/kernel.c:93-128, 358-386) into the
+// split-nibble layout + slice sums; returns scale_x.
+template <int C>
+__device__ float pro_quant(const float4 (&xv)[C], const float4 (&gv)[C], float rms, int K,
+                           const Lds& l) {
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, n4 = K >> 2;
+  float4 v[C];
   float mx = 0.0f;
-  for (int i = tid; i < K; i += nt)
-    mx = fmaxf(mx, fabsf(__fmul_rn(__fmul_rn(p.xs[i], rms), gamma[i])));
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    v[i] = scale4(xv[i], rms, gv[i]);
+    if (tid + i * nt < n4)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  }
   mx = wave_max_f32(mx);
-  if (lane == 0) p.bc[8 + wave] = mx;  // bc has room: carved 64 bytes after slices
+  if (lane == 0) l.bc[8 + wave] = mx;
   __syncthreads();
   float max_abs = 0.0f;
-  for (int w = 0; w < (nt >> 6); ++w) max_abs = fmaxf(max_abs, p.bc[8 + w]);
+  for (int w = 0; w < (nt >> 6); ++w) max_abs = fmaxf(max_abs, l.bc[8 + w]);
   const float scale_x = cr_divf(127.0f, __fadd_rn(max_abs, 1e-5f));
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = tid + i * nt;
+    if (c < n4)
+      ((uint32_t*)l.q8)[c] = q8_of(v[i].x, scale_x) | (q8_of(v[i].y, scale_x) << 8) |
+                             (q8_of(v[i].z, scale_x) << 16) | (q8_of(v[i].w, scale_x) << 24);
+  }
+  __syncthreads();
+  // 16 columns per thread from one 16-byte LDS read -> split nibbles
   const int n_groups = K >> 4;
   for (int g0 = 0; g0 < n_groups; g0 += nt) {
     const int g = g0 + tid;
     int qsum = 0;
     if (g < n_groups) {
+      const uint4 raw = *(const uint4*)(l.q8 + 16 * g);
+      const uint32_t wds[4] = {raw.x, raw.y, raw.z, raw.w};
       int q[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int c = 16 * g + j;
-        const float v = __fmul_rn(__fmul_rn(p.xs[c], rms), gamma[c]);
-        const float t = __fmul_rn(v, scale_x);
-        int iv = (int)__fadd_rn(t, t >= 0.0f ? 0.5f : -0.5f);
-        iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
-        q[j] = iv;
-        qsum += iv;
+        q[j] = (int)(int8_t)(wds[j >> 2] >> (8 * (j & 3)));
+        qsum += q[j];
       }
       uint32_t le = 0, lo = 0, he = 0, ho = 0;
 #pragma unroll
@@ -148,15 +249,19 @@ __device__ float prologue_quant(const Prologue& p, int K, const float* __restric
         he |= (uint32_t)((q[2 * n] >> 4) & 15) << (4 * n);
         ho |= (uint32_t)((q[2 * n + 1] >> 4) & 15) << (4 * n);
       }
-      *(uint4*)(p.nib + 4 * g) = make_uint4(le, lo, he, ho);
+      *(uint4*)(l.nib + 4 * g) = make_uint4(le, lo, he, ho);
     }
     const int s = wave_sum_i32(qsum);  // one wave = 64 groups = one slice
     const int slice = (g0 >> 6) + wave;
-    if (lane == 0 && slice < slices_of(K)) p.slices[slice] = s;
+    if (lane == 0 && slice < slices_of(K)) l.slices[slice] = s;
   }
   __syncthreads();
   return scale_x;
 }
+
+// ---------------------------------------------------------------------------
+// GEMV pieces
+// ---------------------------------------------------------------------------
 
 // x.code over one lane's 64 columns (16 packed bytes, split-nibble act)
 __device__ __forceinline__ int dot64(uint4 w, const uint32_t (&xa)[16]) {
@@ -175,9 +280,9 @@ __device__ __forceinline__ int dot64(uint4 w, const uint32_t (&xa)[16]) {
   return ah * 16 + (int)al;
 }
 
-// Row dot product finish: reduce a lane partial over its 16-lane slice
-// group, subtract the slice's sum of x, fold the slices of the T-lane row
-// team in slice order into fp32 (src/kernel.c:255-256, 407-425).
+// reduce a lane partial over its 16-lane slice group, subtract the slice's
+// sum of x, fold the slices of the T-lane row team in order into fp32
+// (src/kernel.c:255-256, 407-425)
 template <int T>
 __device__ __forceinline__ float row_finish(int part, int xs_slice, int p_index, int n_slices,
                                             float inv, float o, int unit_base) {
@@ -194,149 +299,41 @@ __device__ __forceinline__ float row_finish(int part, int xs_slice, int p_index,
   return o;
 }
 
-// lane activations of the chunks it owns: nib groups 4j..4j+3
 template <int P, int T>
-__device__ __forceinline__ void load_lane_act(const Prologue& pr, int K, int u,
-                                              uint32_t (&xa)[P][16], int (&xsl)[P]) {
+__device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32_t (&xa)[P][16],
+                                              int (&xsl)[P]) {
   const int chunks = K >> 6;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int j = p * T + u;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const uint4 v = j < chunks ? *(const uint4*)(pr.nib + 16 * j + 4 * g) : make_uint4(0, 0, 0, 0);
+      const uint4 v = j < chunks ? *(const uint4*)(l.nib + 16 * j + 4 * g) : make_uint4(0, 0, 0, 0);
       xa[p][4 * g + 0] = v.x;
       xa[p][4 * g + 1] = v.y;
       xa[p][4 * g + 2] = v.z;
       xa[p][4 * g + 3] = v.w;
     }
     const int sl = (p * T + u) >> 4;
-    xsl[p] = sl < slices_of(K) ? pr.slices[sl] : 0;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// in_proj GEMV + SSM step, one block per head.
-//   rows of head h in the device copy: [z (hd) | x (hd) | B | C | dt]
-// ---------------------------------------------------------------------------
-template <int T, int P, int NPF>
-__global__ __launch_bounds__(1024) void k_inproj_ssm(
-    const float* __restrict__ x, int K, const float* __restrict__ gamma,
-    const uint8_t* __restrict__ W, float w_scale, int hd, int di, const float* __restrict__ dt_bias,
-    const float* __restrict__ A, const float* __restrict__ cw, const float* __restrict__ cb,
-    float* __restrict__ cs, float* __restrict__ ssm, const float* __restrict__ D,
-    float* __restrict__ y, const int* __restrict__ ctl) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int RPW = 64 / T;
-  const int h = blockIdx.x;
-  const int rows = 2 * hd + 3;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-  const int u = lane % T, sub = lane / T, unit_base = sub * T;
-  const int n_groups = (rows + RPW - 1) / RPW;
-  const size_t wstride = (size_t)(K >> 2);
-  const uint8_t* __restrict__ Wh = W + (size_t)h * rows * wstride;
-  const int chunks = K >> 6;
-
-  // weight prefetch: this wave's first NPF row groups
-  uint4 wv[NPF][P];
-#pragma unroll
-  for (int it = 0; it < NPF; ++it) {
-    const int r = (wave + it * nwaves) * RPW + sub;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int j = p * T + u;
-      wv[it][p] = (r < rows && j < chunks) ? *(const uint4*)(Wh + (size_t)r * wstride + 16 * j)
-                                           : make_uint4(0, 0, 0, 0);
-    }
-  }
-
-  Prologue pr = prologue_carve(lds, K);
-  float* pj = (float*)(lds + prologue_lds_bytes(K));  // [rows] projections of this head
-  for (int i = tid; i < K; i += blockDim.x) pr.xs[i] = x[i];
-  const float rms = prologue_rms(pr, K);
-  const float scale_x = prologue_quant(pr, K, gamma, rms);
-  const float inv = inv_scale_of(scale_x, w_scale);
-
-  uint32_t xa[P][16];
-  int xsl[P];
-  load_lane_act<P, T>(pr, K, u, xa, xsl);
-
-#pragma unroll
-  for (int it = 0; it < NPF; ++it) {
-    const int grp = wave + it * nwaves;
-    const int r = grp * RPW + sub;
-    if (grp < n_groups) {  // uniform per wave
-      float o = 0.0f;
-#pragma unroll
-      for (int p = 0; p < P; ++p)
-        o = row_finish<T>(dot64(wv[it][p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
-      if (u == 0 && r < rows) pj[r] = o;
-    }
-  }
-  // groups past the prefetched ones (none at the model shapes)
-  for (int grp = wave + NPF * nwaves; grp < n_groups; grp += nwaves) {
-    const int r = grp * RPW + sub;
-    float o = 0.0f;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int j = p * T + u;
-      const uint4 w = (r < rows && j < chunks) ? *(const uint4*)(Wh + (size_t)r * wstride + 16 * j)
-                                               : make_uint4(0, 0, 0, 0);
-      o = row_finish<T>(dot64(w, xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
-    }
-    if (u == 0 && r < rows) pj[r] = o;
-  }
-  __syncthreads();
-
-  // SSM step for the hd channels of this head (src/kernel.c:46-69)
-  if (tid < hd) {
-    const int c = tid, idx = h * hd + c;
-    const int pos = ctl[CTL_POS];
-    const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
-    const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
-    const float dt_val = softplus_r(__fadd_rn(pj[2 * hd + 2], dt_bias[h]));
-    const float decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
-    const float Bdt = __fmul_rn(pj[2 * hd], dt_val);
-    const float C_val = pj[2 * hd + 1];
-    const float xin = pj[hd + c];
-    float* c0 = cs + (size_t)pos * di;
-    float conv = __fadd_rn(cb[idx], __fmul_rn(c0[idx], cw[idx]));
-    conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t1 * di + idx], cw[di + idx]));
-    conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t2 * di + idx], cw[2 * di + idx]));
-    conv = __fadd_rn(conv, __fmul_rn(xin, cw[3 * di + idx]));
-    c0[idx] = xin;
-    const float xa_ = silu_r(conv);
-    const float st = __fadd_rn(__fmul_rn(ssm[idx], decay), __fmul_rn(xa_, Bdt));
-    ssm[idx] = st;
-    y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xa_, D[idx])), silu_r(pj[c]));
+    xsl[p] = sl < slices_of(K) ? l.slices[sl] : 0;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Quantize + GEMV over a slice of rows, 256 threads per block.
-//   PRENORM: input first goes through RMSNorm(norm_f) (the reference's final
-//            norm), then the BitLinear's own norm.
+//   PRENORM: the input first goes through RMSNorm(gamma_pre) -- the
+//            reference's final norm -- then the BitLinear's own norm
 //   MODE:    0 store, 1 accumulate (residual)
-//   ARGMAX:  greedy pick over all rows; the last block finishes the step
+//   PICK:    each block also writes its first-max row (value, index)
 // ---------------------------------------------------------------------------
-struct StepIO {
-  int* ctl;
-  int* hist;
-  int* out_tokens;
-  float* part_v;  // [gridDim.x]
-  int* part_i;
-  const float* embed;  // next token's embedding row goes to x_next
-  float* x_next;
-  int dm;
-};
-
-template <int T, int P, bool PRENORM, int MODE, bool ARGMAX>
+template <int T, int P, int NPF, int C, bool PRENORM, int MODE, bool PICK>
 __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma_pre,
                                                     const float* __restrict__ gamma,
                                                     const uint8_t* __restrict__ W, int N,
                                                     float w_scale, float* __restrict__ out,
-                                                    StepIO io) {
+                                                    float* __restrict__ part_v,
+                                                    int* __restrict__ part_i) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int RPW = 64 / T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -347,71 +344,82 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   const size_t wstride = (size_t)(K >> 2);
   const int chunks = K >> 6;
 
-  // prefetch the first row group of this wave
-  uint4 w[P];
-  {
-    const int r = (g0 + wave) * RPW + sub;
+  // the input vectors first (the prologue waits for them), then the weights
+  float4 sx[C], sg[C], sg2[PRENORM ? C : 1];
+  stage_load<C>(sx, x, K);
+  stage_load<C>(sg, PRENORM ? gamma_pre : gamma, K);
+  if constexpr (PRENORM) stage_load<C>(sg2, gamma, K);
+
+  uint4 wv[NPF][P];
+#pragma unroll
+  for (int it = 0; it < NPF; ++it) {
+    const int grp = g0 + wave + 4 * it;
+    const int r = grp * RPW + sub;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int j = p * T + u;
-      w[p] = (g0 + wave < g1 && r < N && j < chunks)
-                 ? *(const uint4*)(W + (size_t)r * wstride + 16 * j)
-                 : make_uint4(0, 0, 0, 0);
+      wv[it][p] = (grp < g1 && r < N && j < chunks)
+                      ? *(const uint4*)(W + (size_t)r * wstride + 16 * j)
+                      : make_uint4(0, 0, 0, 0);
     }
   }
 
-  Prologue pr = prologue_carve(lds, K);
-  for (int i = tid; i < K; i += blockDim.x) pr.xs[i] = x[i];
-  float rms = prologue_rms(pr, K);
-  if (PRENORM) {
-    // final_feat = (x * rms) * norm_f  (src/model.c:1225, src/kernel.c:93-103)
-    for (int i = tid; i < K; i += blockDim.x)
-      pr.xs[i] = __fmul_rn(__fmul_rn(pr.xs[i], rms), gamma_pre[i]);
-    __syncthreads();
-    rms = prologue_rms(pr, K);
+  const Lds l = lds_carve(lds, K);
+  float rms = pro_rms<C>(sx, K, l);
+  float scale_x;
+  if constexpr (PRENORM) {
+    // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
+#pragma unroll
+    for (int i = 0; i < C; ++i) sx[i] = scale4(sx[i], rms, sg[i]);
+    rms = pro_rms<C>(sx, K, l);
+    scale_x = pro_quant<C>(sx, sg2, rms, K, l);
+  } else {
+    scale_x = pro_quant<C>(sx, sg, rms, K, l);
   }
-  const float scale_x = prologue_quant(pr, K, gamma, rms);
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
   int xsl[P];
-  load_lane_act<P, T>(pr, K, u, xa, xsl);
+  load_lane_act<P, T>(l, K, u, xa, xsl);
 
   float best_v = -1e9f;
   int best_i = 0x7fffffff;
-  for (int grp = g0 + wave; grp < g1; grp += 4) {
-    const int r = grp * RPW + sub;
-    // next group's weights while this one computes
-    uint4 wn[P];
-    const int rn = (grp + 4) * RPW + sub;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int j = p * T + u;
-      wn[p] = (grp + 4 < g1 && rn < N && j < chunks)
-                  ? *(const uint4*)(W + (size_t)rn * wstride + 16 * j)
-                  : make_uint4(0, 0, 0, 0);
-    }
-    float o = 0.0f;
-#pragma unroll
-    for (int p = 0; p < P; ++p)
-      o = row_finish<T>(dot64(w[p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+  auto emit = [&](int r, float o) {
     if (u == 0 && r < N) {
       if (MODE == 1)
         out[r] = __fadd_rn(out[r], o);
       else
         out[r] = o;
-      if (ARGMAX && o > best_v) {  // rows ascend per lane: first max kept
+      if (PICK && o > best_v) {  // rows ascend per lane: first max kept
         best_v = o;
         best_i = r;
       }
     }
+  };
 #pragma unroll
-    for (int p = 0; p < P; ++p) w[p] = wn[p];
+  for (int it = 0; it < NPF; ++it) {
+    const int grp = g0 + wave + 4 * it;
+    if (grp < g1) {  // uniform per wave
+      float o = 0.0f;
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        o = row_finish<T>(dot64(wv[it][p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+      emit(grp * RPW + sub, o);
+    }
+  }
+  for (int grp = g0 + wave + 4 * NPF; grp < g1; grp += 4) {  // beyond the prefetch
+    const int r = grp * RPW + sub;
+    float o = 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = p * T + u;
+      const uint4 w = (r < N && j < chunks) ? *(const uint4*)(W + (size_t)r * wstride + 16 * j)
+                                            : make_uint4(0, 0, 0, 0);
+      o = row_finish<T>(dot64(w, xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+    }
+    emit(r, o);
   }
 
-  if (ARGMAX) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    __shared__ int s_last;
+  if constexpr (PICK) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
       const float ov = __shfl_xor(best_v, o, 64);
@@ -422,152 +430,198 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       }
     }
     if (lane == 0) {
-      sv[wave] = best_v;
-      si[wave] = best_i;
+      l.bc[16 + wave] = best_v;
+      ((int*)l.bc)[20 + wave] = best_i;
     }
     __syncthreads();
     if (tid == 0) {
-      for (int k = 1; k < 4; ++k)
-        if (sv[k] > best_v || (sv[k] == best_v && si[k] < best_i)) {
-          best_v = sv[k];
-          best_i = si[k];
+      for (int k = 1; k < 4; ++k) {
+        const float v = l.bc[16 + k];
+        const int i = ((int*)l.bc)[20 + k];
+        if (v > best_v || (v == best_v && i < best_i)) {
+          best_v = v;
+          best_i = i;
         }
-      io.part_v[blockIdx.x] = best_v;
-      io.part_i[blockIdx.x] = best_i;
-      __threadfence();
-      const int t = atomicAdd(io.ctl + CTL_TICKET, 1);
-      s_last = (t == (int)gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    // last block: reduce the per-block candidates (block order = row order)
-    float bv = -1e9f;
-    int bi = 0x7fffffff;
-    for (int b = tid; b < (int)gridDim.x; b += blockDim.x) {
-      const float v = io.part_v[b];
-      const int i = io.part_i[b];
-      if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
       }
+      part_v[blockIdx.x] = best_v;
+      part_i[blockIdx.x] = best_i;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    __syncthreads();
-    if (lane == 0) {
-      sv[wave] = bv;
-      si[wave] = bi;
-    }
-    __syncthreads();
-    __shared__ int s_tok;
-    if (tid == 0) {
-      for (int k = 1; k < 4; ++k)
-        if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) {
-          bv = sv[k];
-          bi = si[k];
-        }
-      const int best = bi == 0x7fffffff ? 0 : bi;
-      int* ctl = io.ctl;
-      const int step = ctl[CTL_STEP];
-      if (io.out_tokens) io.out_tokens[step] = best;
-      ctl[CTL_STEP] = step + 1;
-      ctl[CTL_TOKEN] = best;
-      io.hist[ctl[CTL_HCOUNT] % kHist] = best;
-      ctl[CTL_HCOUNT] += 1;
-      ctl[CTL_POS] = ctl[CTL_POS] + 1 < 3 ? ctl[CTL_POS] + 1 : 0;  // src/block.c:107
-      ctl[CTL_TICKET] = 0;
-      s_tok = best;
-    }
-    __syncthreads();
-    // next step's input: x = embed[token] (src/model.c:1195-1202)
-    const int tok = s_tok;
-    for (int i = tid; i < io.dm; i += blockDim.x)
-      io.x_next[i] = io.embed[(size_t)tok * io.dm + i];
   }
+}
+
+// ---------------------------------------------------------------------------
+// SSM step, one block per head, one thread per channel.  proj holds the
+// in_proj outputs per head as [z (hd) | x (hd) | B | C | dt].
+// ---------------------------------------------------------------------------
+__global__ void k_ssm_heads(const float* __restrict__ proj, int hd, int di,
+                            const float* __restrict__ dt_bias, const float* __restrict__ A,
+                            const float* __restrict__ cw, const float* __restrict__ cb,
+                            float* __restrict__ cs, float* __restrict__ ssm,
+                            const float* __restrict__ D, float* __restrict__ y,
+                            const int* __restrict__ ctl) {
+  const int h = blockIdx.x, c = threadIdx.x;
+  if (c >= hd) return;
+  const float* __restrict__ ph = proj + (size_t)h * (2 * hd + 3);
+  const int idx = h * hd + c;
+  const int pos = ctl[CTL_POS];
+  const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
+  const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
+  const float dt_val = softplus_r(__fadd_rn(ph[2 * hd + 2], dt_bias[h]));
+  const float decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
+  const float Bdt = __fmul_rn(ph[2 * hd], dt_val);
+  const float C_val = ph[2 * hd + 1];
+  const float xin = ph[hd + c];
+  float* c0 = cs + (size_t)pos * di;
+  float conv = __fadd_rn(cb[idx], __fmul_rn(c0[idx], cw[idx]));
+  conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t1 * di + idx], cw[di + idx]));
+  conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t2 * di + idx], cw[2 * di + idx]));
+  conv = __fadd_rn(conv, __fmul_rn(xin, cw[3 * di + idx]));
+  c0[idx] = xin;  // the oldest tap is overwritten (cs_write == cs0)
+  const float xa = silu_r(conv);
+  const float st = __fadd_rn(__fmul_rn(ssm[idx], decay), __fmul_rn(xa, Bdt));
+  ssm[idx] = st;
+  y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xa, D[idx])), silu_r(ph[c]));
+}
+
+// ---------------------------------------------------------------------------
+// Greedy pick over the LM-head blocks' candidates (block order = row order,
+// so "greater, or equal with a lower index" keeps the first maximum), then
+// the step bookkeeping and x = embed[token] (src/model.c:1195-1202).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
+                                              const int* __restrict__ part_i, int n_parts,
+                                              int* __restrict__ ctl, int* __restrict__ hist,
+                                              int* __restrict__ out_tokens,
+                                              const float* __restrict__ embed, int dm,
+                                              float* __restrict__ x) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  __shared__ int s_tok;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float bv = -1e9f;
+  int bi = 0x7fffffff;
+  for (int b = tid; b < n_parts; b += blockDim.x) {
+    const float v = part_v[b];
+    const int i = part_i[b];
+    if (v > bv || (v == bv && i < bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int k = 1; k < 4; ++k)
+      if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) {
+        bv = sv[k];
+        bi = si[k];
+      }
+    const int best = bi == 0x7fffffff ? 0 : bi;
+    const int step = ctl[CTL_STEP];
+    if (out_tokens) out_tokens[step] = best;
+    ctl[CTL_STEP] = step + 1;
+    ctl[CTL_TOKEN] = best;
+    hist[ctl[CTL_HCOUNT] % kHist] = best;
+    ctl[CTL_HCOUNT] += 1;
+    ctl[CTL_POS] = ctl[CTL_POS] + 1 < 3 ? ctl[CTL_POS] + 1 : 0;  // src/block.c:107
+    s_tok = best;
+  }
+  __syncthreads();
+  const int tok = s_tok;
+  for (int i = tid; i < dm; i += blockDim.x) x[i] = embed[(size_t)tok * dm + i];
 }
 
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
-                             float w_scale, int nh, int hd, const float* dt_bias,
-                             const float* A, const float* cw, const float* cb, float* cs,
-                             float* ssm, const float* D, float* y, const int* ctl,
-                             hipStream_t s) {
-  const int di = nh * hd;
-  const size_t lds = prologue_lds_bytes(K) + 4 * (size_t)(2 * hd + 3) + 16;
-  const dim3 grid(nh), block(1024);
-  if (K <= 1024)
-    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       hd, di, dt_bias, A, cw, cb, cs, ssm, D, y, ctl);
-  else if (K <= 2048)
-    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       hd, di, dt_bias, A, cw, cb, cs, ssm, D, y, ctl);
-  else if (K <= 4096)
-    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       hd, di, dt_bias, A, cw, cb, cs, ssm, D, y, ctl);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
-}
 
-template <bool PRENORM, int MODE, bool ARGMAX>
-static hipError_t rows_fused_t(const float* x, int K, const float* gpre, const float* g,
-                               const uint8_t* W, int N, float w_scale, float* out, StepIO io,
-                               int blocks, hipStream_t s) {
-  const size_t lds = prologue_lds_bytes(K);
-  if (K <= 1024)
-    hipLaunchKernelGGL((k_rows_fused<16, 1, PRENORM, MODE, ARGMAX>), dim3(blocks), dim3(256),
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, io);
-  else if (K <= 2048)
-    hipLaunchKernelGGL((k_rows_fused<32, 1, PRENORM, MODE, ARGMAX>), dim3(blocks), dim3(256),
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, io);
-  else if (K <= 4096)
-    hipLaunchKernelGGL((k_rows_fused<64, 1, PRENORM, MODE, ARGMAX>), dim3(blocks), dim3(256),
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, io);
-  else if (K <= 8192)
-    hipLaunchKernelGGL((k_rows_fused<64, 2, PRENORM, MODE, ARGMAX>), dim3(blocks), dim3(256),
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, io);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
-}
-
-// out (+)= BitLinear(x) over N rows; blocks chosen for the row count
-hipError_t launch_rows_fused(const float* x, int K, const float* gamma, const uint8_t* W, int N,
-                             float w_scale, float* out, bool accumulate, hipStream_t s) {
-  StepIO io{};
+// blocks such that each of the 4 waves owns at most NPF row groups
+template <int NPF>
+static int rows_blocks(int N, int K) {
   const int rpw = K <= 1024 ? 4 : (K <= 2048 ? 2 : 1);
-  int blocks = (N / rpw + 7) / 8;  // ~2 row groups per wave
-  if (blocks > 256) blocks = 256;
-  if (blocks < 1) blocks = 1;
-  if (accumulate)
-    return rows_fused_t<false, 1, false>(x, K, nullptr, gamma, W, N, w_scale, out, io, blocks, s);
-  return rows_fused_t<false, 0, false>(x, K, nullptr, gamma, W, N, w_scale, out, io, blocks, s);
+  const int G = (N + rpw - 1) / rpw;
+  int b = (G + 4 * NPF - 1) / (4 * NPF);
+  return b < 1 ? 1 : b;
 }
 
-// LM head: RMSNorm(norm_f) + BitLinear(lm_head) -> logits, then (argmax)
-// the greedy step bookkeeping and the next token's embedding
+template <int NPF, bool PRENORM, int MODE, bool PICK>
+static hipError_t rows_t(const float* x, int K, const float* gpre, const float* g,
+                         const uint8_t* W, int N, float w_scale, float* out, float* pv, int* pi,
+                         hipStream_t s) {
+  const size_t lds = lds_bytes(K);
+  const dim3 grid(rows_blocks<NPF>(N, K)), block(256);
+  if (K % 64 != 0) return hipErrorInvalidValue;
+  if (K <= 1024)
+    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK>), grid, block, lds, s, x,
+                       K, gpre, g, W, N, w_scale, out, pv, pi);
+  else if (K <= 2048)
+    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK>), grid, block, lds, s, x,
+                       K, gpre, g, W, N, w_scale, out, pv, pi);
+  else if (K <= 4096)
+    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK>), grid, block, lds, s, x,
+                       K, gpre, g, W, N, w_scale, out, pv, pi);
+  else if (K <= 8192)
+    hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK>), grid, block, lds, s, x,
+                       K, gpre, g, W, N, w_scale, out, pv, pi);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// proj = BitLinear(x) over the per-head in_proj rows
+hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_t* W, int N,
+                         float w_scale, float* proj, hipStream_t s) {
+  return rows_t<4, false, 0, false>(x, K, nullptr, gamma, W, N, w_scale, proj, nullptr, nullptr,
+                                    s);
+}
+
+// x += BitLinear(y)  (out_proj with the residual add)
+hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
+                          float w_scale, float* x, hipStream_t s) {
+  return rows_t<2, false, 1, false>(y, K, nullptr, gamma, W, N, w_scale, x, nullptr, nullptr, s);
+}
+
+hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
+                            const float* A, const float* cw, const float* cb, float* cs,
+                            float* ssm, const float* D, float* y, const int* ctl, hipStream_t s) {
+  if (hd > 1024) return hipErrorInvalidValue;
+  const int threads = (hd + 63) / 64 * 64;
+  hipLaunchKernelGGL(k_ssm_heads, dim3(nh), dim3(threads), 0, s, proj, hd, nh * hd, dt_bias, A,
+                     cw, cb, cs, ssm, D, y, ctl);
+  return hipGetLastError();
+}
+
+// LM head: logits = BitLinear(RMSNorm(x; norm_f); lm_head), plus per-block
+// greedy candidates when pick is set
+int lm_head_blocks(int N, int K) { return rows_blocks<16>(N, K); }
+
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
-                          const uint8_t* W, int N, float w_scale, float* logits, bool argmax,
-                          int* ctl, int* hist, int* out_tokens, float* part_v, int* part_i,
-                          const float* embed, float* x_next, int blocks, hipStream_t s) {
-  StepIO io{ctl, hist, out_tokens, part_v, part_i, embed, x_next, K};
-  if (argmax)
-    return rows_fused_t<true, 0, true>(x, K, norm_f, lm_norm, W, N, w_scale, logits, io, blocks,
-                                       s);
-  return rows_fused_t<true, 0, false>(x, K, norm_f, lm_norm, W, N, w_scale, logits, io, blocks,
-                                      s);
+                          const uint8_t* W, int N, float w_scale, float* logits, bool pick,
+                          float* part_v, int* part_i, hipStream_t s) {
+  if (pick)
+    return rows_t<16, true, 0, true>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
+                                     s);
+  return rows_t<16, true, 0, false>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr,
+                                    nullptr, s);
 }
 
-size_t decode_prologue_lds(int K) { return prologue_lds_bytes(K); }
+hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,
+                       int* out_tokens, const float* embed, int dm, float* x, hipStream_t s) {
+  hipLaunchKernelGGL(k_pick, dim3(1), dim3(256), 0, s, part_v, part_i, n_parts, ctl, hist,
+                     out_tokens, embed, dm, x);
+  return hipGetLastError();
+}
 
 }  // namespace bm

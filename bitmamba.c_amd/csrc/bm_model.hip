@@ -176,17 +176,19 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ 
   }
 }
 
-hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
-                             float w_scale, int nh, int hd, const float* dt_bias,
-                             const float* A, const float* cw, const float* cb, float* cs,
-                             float* ssm, const float* D, float* y, const int* ctl,
-                             hipStream_t s);
-hipError_t launch_rows_fused(const float* x, int K, const float* gamma, const uint8_t* W, int N,
-                             float w_scale, float* out, bool accumulate, hipStream_t s);
+hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_t* W, int N,
+                         float w_scale, float* proj, hipStream_t s);
+hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
+                          float w_scale, float* x, hipStream_t s);
+hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
+                            const float* A, const float* cw, const float* cb, float* cs,
+                            float* ssm, const float* D, float* y, const int* ctl, hipStream_t s);
+int lm_head_blocks(int N, int K);
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
-                          const uint8_t* W, int N, float w_scale, float* logits, bool argmax,
-                          int* ctl, int* hist, int* out_tokens, float* part_v, int* part_i,
-                          const float* embed, float* x_next, int blocks, hipStream_t s);
+                          const uint8_t* W, int N, float w_scale, float* logits, bool pick,
+                          float* part_v, int* part_i, hipStream_t s);
+hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,
+                       int* out_tokens, const float* embed, int dm, float* x, hipStream_t s);
 
 }  // namespace bm
 
@@ -221,6 +223,7 @@ struct bm_hip_model {
   float *x = nullptr, *proj = nullptr, *y = nullptr, *feat = nullptr, *logits = nullptr;
   float* part_v = nullptr;  // per-block greedy candidates of the LM head
   int* part_i = nullptr;
+  int lm_blocks = 0;
   float* scale = nullptr;
   uint8_t* act = nullptr;
   int8_t* xq = nullptr;
@@ -270,7 +273,6 @@ int bitlinear(bm_hip_model* m, const float* x, int M, int K, const float* norm,
   return 0;
 }
 
-constexpr int kLmBlocks = 256;
 
 // The kernels of one decode step, enqueued on s.  m->x already holds the
 // embedding of the current token.
@@ -280,24 +282,25 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
     const Layer& Ly = m->L[l];
     float* cs = m->conv_state + (size_t)l * 3 * di;
     float* ss = m->ssm_state + (size_t)l * di;
-    // block_step, unfused branch (src/block.c:361-371) + residual
-    MCHECK(bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
-                                 Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
-                                 m->ctl, s));
-    MCHECK(bm::launch_rows_fused(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x,
-                                 true, s));
+    // block_step, unfused branch (src/block.c:361-371), then the residual
+    MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj, s));
+    MCHECK(bm::launch_ssm_heads(m->proj, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b,
+                                cs, ss, Ly.D, m->y, m->ctl, s));
+    MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s));
   }
   const bool fused_pick = penalty == 1.0f;  // x / 1.0f == x * 1.0f == x
   MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab, m->lm_scale,
-                            m->logits, fused_pick, m->ctl, m->hist,
-                            write_out ? m->out_tokens : nullptr, m->part_v, m->part_i, m->embed,
-                            m->x, kLmBlocks, s));
-  if (!fused_pick) {
+                            m->logits, fused_pick, m->part_v, m->part_i, s));
+  int* out = write_out ? m->out_tokens : nullptr;
+  if (fused_pick) {
+    MCHECK(bm::launch_pick(m->part_v, m->part_i, m->lm_blocks, m->ctl, m->hist, out, m->embed, dm,
+                           m->x, s));
+  } else {
     hipLaunchKernelGGL(bm::k_penalty, dim3(1), dim3(bm::kHistory), 0, s, m->logits, m->vocab,
                        m->hist, m->ctl, penalty);
     MCHECK(hipGetLastError());
     hipLaunchKernelGGL(bm::k_argmax_step, dim3(1), dim3(1024), 0, s, m->logits, m->vocab, m->ctl,
-                       m->hist, write_out ? m->out_tokens : nullptr);
+                       m->hist, out);
     MCHECK(hipGetLastError());
     hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, 1), dim3(256), 0, s, m->embed, dm,
                        m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
@@ -501,8 +504,9 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
   MCHECK(hipMalloc(&m->y, (size_t)di * 4));
   MCHECK(hipMalloc(&m->feat, (size_t)dm * 4));
   MCHECK(hipMalloc(&m->logits, (size_t)m->vocab * 4));
-  MCHECK(hipMalloc(&m->part_v, kLmBlocks * 4));
-  MCHECK(hipMalloc(&m->part_i, kLmBlocks * 4));
+  m->lm_blocks = bm::lm_head_blocks(m->vocab, dm);
+  MCHECK(hipMalloc(&m->part_v, (size_t)m->lm_blocks * 4));
+  MCHECK(hipMalloc(&m->part_i, (size_t)m->lm_blocks * 4));
   MCHECK(hipMalloc(&m->scale, 64));
   MCHECK(hipMalloc(&m->act, bm::act_row_bytes(di > dm ? di : dm)));
   MCHECK(hipMalloc(&m->xq, (size_t)(di > dm ? di : dm)));
