@@ -119,7 +119,7 @@ def leg_roofline(L, reps=5):
         b.free()
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
-                kernel="k_gemv<32,1,2,canonical,store> (K=2048 decode GEMV)",
+                kernel="k_gemv<T=32,P=1,GW=8,canonical,store> (K=2048 decode GEMV, 8 row groups per wave)",
                 bytes_per_launch=wbytes, launch_us=round(ms * 1e3, 2),
                 rows_per_launch=N)
 

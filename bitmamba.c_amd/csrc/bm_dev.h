@@ -9,6 +9,12 @@ namespace bm {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// 16-byte streaming load (nontemporal: weights are read once per pass)
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  const v4i v = __builtin_nontemporal_load((const v4i*)p);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
 __device__ __forceinline__ uint32_t canon_codes(uint32_t p) {
   // field 11 -> 10: clear the low bit where both bits are set
   return p - (((p >> 1) & p) & 0x55555555u);

@@ -13,6 +13,8 @@
 // 27-31).  Kernels compute x.w = x.code - sum(x) with code in {0,1,2}; a
 // code 11 is rewritten to 10 first (same value) unless the caller promises
 // canonical weights.
+#include <type_traits>
+
 #include "bm_common.h"
 #include "bm_dev.h"
 
@@ -162,20 +164,24 @@ __global__ __launch_bounds__(QT) void k_prep_i8(const int8_t* __restrict__ xq, i
 //   T lanes per row (16/32/64), each lane owns 64 columns (16 packed bytes)
 //   per pass; P passes cover K.  16 consecutive lanes = one 1024-column
 //   slice, reduced with xor shuffles inside the 16-lane group.
+//   Each wave owns GW consecutive row groups (64/T rows each) and issues
+//   all of their weight loads before the first dot product, so a wave keeps
+//   GW KiB (T=32) in flight and never waits on its own stores.
 // ---------------------------------------------------------------------------
-template <int T, int P, int UNR, bool CANON, int MODE>
+template <int T, int P, int GW, bool CANON, int MODE>
 __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, size_t act_stride,
                                               const float* __restrict__ scale_x,
                                               const uint8_t* __restrict__ W, int N, int K,
                                               float w_scale, float* __restrict__ out,
                                               int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
-  constexpr int RPW = 64 / T;  // rows per wave per row-group
+  constexpr int RPW = 64 / T;  // rows per wave per row group
   const int m = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int u = lane % T, sub = lane / T, unit_base = sub * T;
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int n_waves = gridDim.x * 4;
+  const int n_rg = (N + RPW - 1) / RPW;
+  const int rg0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GW;
+  if (rg0 >= n_rg) return;
   const int chunks = K >> 6;
   const size_t wstride = (size_t)(K >> 2);
 
@@ -201,70 +207,72 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, s
     const int slice = (p * T + u) / 16;
     xs[p] = slice < slices_of(K) ? ssum[slice] : 0;
   }
+
+  // weights of all GW row groups.  Rows past N reread row N-1 and are never
+  // stored; lanes past the last chunk read the last chunk, which meets zero
+  // activations.
+  uint4 wv[GW][P];
+#pragma unroll
+  for (int i = 0; i < GW; ++i) {
+    const int r = min((rg0 + i) * RPW + sub, N - 1);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = min(p * T + u, chunks - 1);
+      wv[i][p] = load_stream16(W + (size_t)r * wstride + 16 * (size_t)j);
+    }
+  }
   const float inv = I32 ? 0.0f : inv_scale_of(scale_x[m], w_scale);
 
-  const int n_rg = (N + RPW - 1) / RPW;
-  for (int base = gw; base < n_rg; base += n_waves * UNR) {
-    uint4 wv[UNR][P];
-    int rows[UNR];
+  float o[GW];
+  int tot[GW];
 #pragma unroll
-    for (int i = 0; i < UNR; ++i) {
-      const int rg = base + i * n_waves;
-      rows[i] = rg * RPW + sub;
-      const bool ok = rg < n_rg && rows[i] < N;
+  for (int i = 0; i < GW; ++i) {
+    o[i] = 0.0f;
+    tot[i] = 0;
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const int j = p * T + u;
-        wv[i][p] = (ok && j < chunks)
-                       ? *(const uint4*)(W + (size_t)rows[i] * wstride + 16 * (size_t)j)
-                       : make_uint4(0, 0, 0, 0);
+    for (int p = 0; p < P; ++p) {
+      const uint32_t w4[4] = {wv[i][p].x, wv[i][p].y, wv[i][p].z, wv[i][p].w};
+      uint32_t al = 0;
+      int ah = 0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t pw = CANON ? w4[d] : canon_codes(w4[d]);
+        const uint32_t lo = pw & 0x33333333u;
+        const uint32_t hi = (pw >> 2) & 0x33333333u;
+        al = __builtin_amdgcn_udot8(lo, xa[p][4 * d + 0], al, false);
+        al = __builtin_amdgcn_udot8(hi, xa[p][4 * d + 1], al, false);
+        ah = __builtin_amdgcn_sdot8((int)lo, (int)xa[p][4 * d + 2], ah, false);
+        ah = __builtin_amdgcn_sdot8((int)hi, (int)xa[p][4 * d + 3], ah, false);
+      }
+      int part = ah * 16 + (int)al;
+      part += __shfl_xor(part, 8, 64);
+      part += __shfl_xor(part, 4, 64);
+      part += __shfl_xor(part, 2, 64);
+      part += __shfl_xor(part, 1, 64);
+      const int t = part - xs[p];  // exact slice total of x.w
+      if (I32) {
+#pragma unroll
+        for (int q = 0; q < T / 16; ++q) tot[i] += __shfl(t, unit_base + 16 * q, 64);
+      } else {
+        const float f = __fmul_rn((float)t, inv);
+#pragma unroll
+        for (int q = 0; q < T / 16; ++q) {
+          const float fq = __shfl(f, unit_base + 16 * q, 64);
+          // slices past K contribute nothing (they do not exist there)
+          if (p * (T / 16) + q < slices_of(K)) o[i] = __fadd_rn(o[i], fq);
+        }
       }
     }
+  }
+  if (u == 0) {
 #pragma unroll
-    for (int i = 0; i < UNR; ++i) {
-      float o = 0.0f;
-      int tot = 0;
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const uint32_t w4[4] = {wv[i][p].x, wv[i][p].y, wv[i][p].z, wv[i][p].w};
-        uint32_t al = 0;
-        int ah = 0;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint32_t pw = CANON ? w4[d] : canon_codes(w4[d]);
-          const uint32_t lo = pw & 0x33333333u;
-          const uint32_t hi = (pw >> 2) & 0x33333333u;
-          al = __builtin_amdgcn_udot8(lo, xa[p][4 * d + 0], al, false);
-          al = __builtin_amdgcn_udot8(hi, xa[p][4 * d + 1], al, false);
-          ah = __builtin_amdgcn_sdot8((int)lo, (int)xa[p][4 * d + 2], ah, false);
-          ah = __builtin_amdgcn_sdot8((int)hi, (int)xa[p][4 * d + 3], ah, false);
-        }
-        int part = ah * 16 + (int)al;
-        part += __shfl_xor(part, 8, 64);
-        part += __shfl_xor(part, 4, 64);
-        part += __shfl_xor(part, 2, 64);
-        part += __shfl_xor(part, 1, 64);
-        const int t = part - xs[p];  // exact slice total of x.w
-        if (I32) {
-#pragma unroll
-          for (int q = 0; q < T / 16; ++q) tot += __shfl(t, unit_base + 16 * q, 64);
-        } else {
-          const float f = __fmul_rn((float)t, inv);
-#pragma unroll
-          for (int q = 0; q < T / 16; ++q) {
-            const float fq = __shfl(f, unit_base + 16 * q, 64);
-            // slices past K contribute nothing (they do not exist there)
-            if (p * (T / 16) + q < slices_of(K)) o = __fadd_rn(o, fq);
-          }
-        }
-      }
-      const int rg = base + i * n_waves;
-      if (u == 0 && rg < n_rg && rows[i] < N) {
+    for (int i = 0; i < GW; ++i) {
+      const int row = (rg0 + i) * RPW + sub;
+      if (rg0 + i < n_rg && row < N) {
         if (I32)
-          out_i32[(size_t)m * N + rows[i]] = tot;
+          out_i32[(size_t)m * N + row] = tot[i];
         else
-          out[(size_t)m * N + rows[i]] =
-              MODE == 1 ? __fadd_rn(out[(size_t)m * N + rows[i]], o) : o;
+          out[(size_t)m * N + row] = MODE == 1 ? __fadd_rn(out[(size_t)m * N + row], o[i]) : o[i];
       }
     }
   }
@@ -496,19 +504,26 @@ hipError_t launch_prep_i8(const int8_t* xq, int M, int ldx, int K, uint8_t* act,
   return hipGetLastError();
 }
 
+// rows per wave: as many as keep >= 8 waves per CU busy (256 CUs)
 template <int T, int P, bool CANON, int MODE>
 static hipError_t gemv_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
                          int K, float w_scale, void* out, hipStream_t s) {
   constexpr int RPW = 64 / T;
-  const int n_rg = (N + RPW - 1) / RPW;
-  const int UNR = 2;
-  int waves = (n_rg + UNR - 1) / UNR;
-  int blocks = (waves + 3) / 4;
-  const int cap = 2048;
-  if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL((k_gemv<T, P, 2, CANON, MODE>), dim3(blocks, M), dim3(256), 0, s, act,
-                     act_row_bytes(K), scale_x, W, N, K, w_scale, (float*)out, (int32_t*)out);
-  return hipGetLastError();
+  const long long n_rg = (N + RPW - 1) / RPW;
+  const long long want = 8LL * 256 * 4 / (M < 4 ? M : 4);  // waves wanted in all
+  auto go = [&](auto gw) {
+    constexpr int GW = decltype(gw)::value;
+    const long long waves = (n_rg + GW - 1) / GW;
+    const unsigned blocks = (unsigned)((waves + 3) / 4);
+    hipLaunchKernelGGL((k_gemv<T, P, GW, CANON, MODE>), dim3(blocks, M), dim3(256), 0, s, act,
+                       act_row_bytes(K), scale_x, W, N, K, w_scale, (float*)out, (int32_t*)out);
+    return hipGetLastError();
+  };
+  // (16 groups per wave measured slower than 8: fewer waves fit per SIMD)
+  if (n_rg >= 8 * want) return go(std::integral_constant<int, 8>());
+  if (n_rg >= 4 * want) return go(std::integral_constant<int, 4>());
+  if (n_rg >= 2 * want) return go(std::integral_constant<int, 2>());
+  return go(std::integral_constant<int, 1>());
 }
 
 template <bool CANON, int MODE>
