@@ -16,6 +16,11 @@ Prints ONE JSON line.  Legs (all by default):
   prefill   int8-MFMA GEMM at M=2048: 2048->8512 and 4096->2048, TOP/s
   cpu       the reference's own AVX2 build (oracle/_ref) on the host cores:
             a bounded sample of the same decode workload
+  copy      (on request only) a plain 512 MiB device copy: the calibration
+            run for the HBM traffic counters
+The roofline's `traffic` (HBM bytes per launch of the GEMV) is read from
+profiles/gemv_k2048_traffic.txt, which holds the FETCH_SIZE / WRITE_SIZE
+counter runs of this same leg and their copy-kernel calibration.
 """
 import argparse
 import ctypes as C
@@ -35,6 +40,7 @@ METRIC = "packed-weight GB/s + tok/s (1B-shape decode, bs=1); prefill ternary GE
 CFG_1B = dict(vocab=50257, d_model=2048, n_layers=24, n_heads=64, dist=bh.SYNTH_P0_40,
               seed=1000, prompt=8)
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_k2048_traffic.txt")
 I8_PEAK_TOPS = 5000.0
 
 
@@ -118,10 +124,41 @@ def leg_roofline(L, reps=5):
     for b in (dW, dx, dg, dq, ds, da, dout):
         b.free()
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=None,
+                frac=round(achieved / HBM_PEAK_GBPS, 4), traffic=measured_traffic(N),
                 kernel="k_gemv<T=32,P=1,GW=8,canonical,store> (K=2048 decode GEMV, 8 row groups per wave)",
                 bytes_per_launch=wbytes, launch_us=round(ms * 1e3, 2),
                 rows_per_launch=N)
+
+
+def measured_traffic(rows):
+    """HBM bytes per GEMV launch from the committed counter summary (a line
+    'bytes_per_launch: <int> rows: <int>'), if it covers this shape."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("bytes_per_launch:"):
+                f = line.split()
+                if int(f[3]) == rows:
+                    return int(f[1])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
+def leg_copy(L, reps=5):
+    n = 512 << 20
+    a, b = bh.DeviceBuffer(n), bh.DeviceBuffer(n)
+    bh.check(L.bm_hip_memset(a.ptr, 1, n), "memset")
+    ev = Events(L)
+    for _ in range(2):
+        bh.check(L.bm_hip_copy_dev(b.ptr, a.ptr, n, None), "copy")
+    ev.start()
+    for _ in range(reps):
+        bh.check(L.bm_hip_copy_dev(b.ptr, a.ptr, n, None), "copy")
+    ms = ev.stop_ms() / reps
+    a.free()
+    b.free()
+    return dict(bytes_read=n, bytes_written=n, us=round(ms * 1e3, 1),
+                GBps_read_plus_write=round(2 * n / (ms * 1e-3) / 1e9, 1))
 
 
 def leg_prefill(L, reps=10):
@@ -262,6 +299,9 @@ def main():
     pre = leg_prefill(L) if "prefill" in legs else None
     if pre:
         log("prefill: %s" % json.dumps(pre))
+    cpy = leg_copy(L) if "copy" in legs else None
+    if cpy:
+        log("copy: %s" % json.dumps(cpy))
     cpu = leg_cpu() if "cpu" in legs else None
     if cpu:
         log("cpu baseline: %s" % json.dumps(cpu))
@@ -287,6 +327,8 @@ def main():
     line["roofline"] = roof
     line["prefill_gemm"] = pre
     line["cpu_baseline"] = cpu
+    if cpy:
+        line["copy_calibration"] = cpy
     print(json.dumps(line), flush=True)
 
 

@@ -2,12 +2,15 @@
 // model_prefill / model_forward_step (src/model.c:477-1314, src/block.c)
 // with every activation kept in HBM.
 //
-// Per decoded token the device runs, without a host round trip:
-//   embed -> per layer [quantize x; in_proj GEMV; SSM step; quantize y;
-//   out_proj GEMV accumulated into x] -> RMSNorm(norm_f) -> quantize ->
-//   LM-head GEMV -> repetition penalty -> greedy argmax.
-// The sequence is captured once into a hipGraph and replayed; the current
-// token, conv ring position, step counter and history live in device memory.
+// Per decoded token the device runs, without a host round trip, per layer
+//   k_rows_fused (quantize x + in_proj GEMV) -> k_ssm_heads (SSM step) ->
+//   k_rows_fused (quantize y + out_proj GEMV accumulated into x)
+// then the LM head (RMSNorm(norm_f) + quantize + GEMV, each block keeping
+// its greedy candidate) and k_pick (greedy choice, bookkeeping, embedding of
+// the next token); with a repetition penalty the LM head is followed by
+// k_penalty, k_argmax_step and k_embed instead.  The sequence is captured
+// once into a hipGraph and replayed; the current token, conv ring position,
+// step counter and history live in device memory.
 // Numerics are those of the scalar reference path, bit for bit.
 #include <math.h>
 #include <stdlib.h>
@@ -24,7 +27,7 @@
 namespace bm {
 
 // control block in device memory
-enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_TICKET = 4, CTL_WORDS = 8 };
+enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_WORDS = 8 };
 constexpr int kHistory = 256;  // HISTORY_MAX (src/main.c:19)
 
 __device__ __forceinline__ float silu_ref(float x) {
