@@ -340,113 +340,183 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 
 // ---------------------------------------------------------------------------
 // Prefill / batched GEMM on int8 MFMA (v_mfma_i32_32x32x32_i8).
-//   block 256 threads = 2x2 waves, tile 128(M) x 128(N), K step 128.
-//   A (permuted int8 activations) staged in LDS; B decoded from the packed
-//   bytes straight into MFMA operand registers: a 16-byte load gives a lane
-//   64 columns of one weight row, i.e. its operand for four 32-deep steps.
+//   block 256 threads = 2x2 waves, tile 128(M) x 128(N), each wave 64 x 64
+//   (2 x 2 MFMA tiles); K in stages of 128.
+//   A (permuted int8 activations): each stage is streamed into one of two
+//   LDS buffers by LDS-DMA loads (16 bytes per lane, 1 KiB per wave
+//   instruction), its 16-byte chunks XOR-swizzled by row so the operand
+//   reads of 8 consecutive rows hit 8 different bank groups.  The next
+//   stage is issued right after the current one's operands are in
+//   registers, so one barrier per stage suffices.
+//   B: decoded from the packed bytes straight into operand registers: a
+//   16-byte load gives a lane 64 columns of one weight row, its operand for
+//   the stage's four 32-deep steps; the next stage's bytes are loaded while
+//   the current stage runs.
 //   Lane (j = lane%32, h = lane/32) covers columns kb + 64h + 16s.. in step
-//   s, for A and B alike.  int32 accumulators are folded into fp32 at every
-//   1024-column slice boundary in slice order.
+//   s, for A and B alike.  Codes are used as is (0, 1, 2) and the slice sum
+//   of x is subtracted at each 1024-column slice boundary, where the int32
+//   totals are folded into fp32 in slice order.
 // ---------------------------------------------------------------------------
-constexpr int GBM = 128, GBN = 128, GBK = 128, GLDA = GBK + 16;
+constexpr int GBM = 128, GBN = 128, GBK = 128;
+constexpr int GMAX_SLICES = 16;  // K <= 16384
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 template <bool CANON, int MODE>
-__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ act, size_t act_stride,
-                                              const float* __restrict__ scale_x, int M,
-                                              const uint8_t* __restrict__ W, int N, int K,
-                                              float w_scale, float* __restrict__ out,
-                                              int32_t* __restrict__ out_i32) {
+__global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act,
+                                                 size_t act_stride,
+                                                 const float* __restrict__ scale_x, int M,
+                                                 const uint8_t* __restrict__ W, int N, int K,
+                                                 float w_scale, float* __restrict__ out,
+                                                 int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
-  __shared__ __attribute__((aligned(16))) int8_t sA[GBM * GLDA];
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][GBM * GBK];
+  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES + 1][GBM];  // [S] = total
+  __shared__ __attribute__((aligned(16))) float s_inv[GBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int j32 = lane & 31, h = lane >> 5;
   const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
   const size_t wstride = (size_t)(K >> 2);
   const size_t perm = act_perm_off(K);
+  const int n_slices = slices_of(K);
+  const int n_stages = K / GBK;
+
+  // per-row slice sums of x and 1/(scale_x * w_scale)
+  for (int i = tid; i < GBM * n_slices; i += 256) {
+    const int r = i % GBM, sl = i / GBM;
+    const int row = min(m0 + r, M - 1);
+    s_sx[sl][r] = ((const int*)(act + (size_t)row * act_stride))[sl];
+  }
+  if (tid < GBM) {
+    const int row = min(m0 + tid, M - 1);
+    s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[row], w_scale);
+  }
+
+  // LDS-DMA of one A stage: wave instruction i writes rows 8*(4i+wave) ..+8
+  // as 1 KiB; lane l lands at row l/8, chunk position l%8, and fetches the
+  // chunk (l%8) ^ (l/8) of that row.
+  auto stage_a = [&](int kb, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rl = 8 * (4 * i + wave) + (lane >> 3);
+      const int row = min(m0 + rl, M - 1);
+      const int chunk = (lane & 7) ^ (lane >> 3);
+      const uint8_t* src = act + (size_t)row * act_stride + perm + kb + 16 * chunk;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)src,
+                                       (lds_void_t*)(sA[buf] + 1024 * (4 * i + wave)), 16, 0, 0);
+    }
+  };
+  // packed bytes of the wave's two 32-column weight tiles for one stage
+  auto stage_b = [&](int kb, uint4 (&bw)[2]) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int n = min(n0 + wn * 64 + nt * 32 + j32, N - 1);
+      bw[nt] = *(const uint4*)(W + (size_t)n * wstride + (kb >> 2) + 16 * h);
+    }
+  };
 
   v16i acc[2][2];
   float o[2][2][16];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         acc[a][b][v] = 0;
         o[a][b][v] = 0.0f;
       }
-    }
 
-  // rows of the accumulator elements this lane owns (C layout of 32x32)
-  // row = 8*(v/4) + 4*h + v%4 within the 32-row tile
-  for (int kb = 0; kb < K; kb += GBK) {
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int idx = tid + q * 256;
-      const int row = idx >> 3, c16 = idx & 7;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m0 + row < M)
-        v = *(const uint4*)(act + (size_t)(m0 + row) * act_stride + perm + kb + 16 * c16);
-      *(uint4*)(sA + row * GLDA + 16 * c16) = v;
-    }
-    __syncthreads();
+  uint4 bcur[2], bnext[2];
+  stage_a(0, 0);
+  stage_b(0, bcur);
+  __syncthreads();
 
-    v4i bop[2][4];
+  for (int st = 0; st < n_stages; ++st) {
+    const int kb = st * GBK;
+    const uint8_t* __restrict__ cur = sA[st & 1];
+    // this stage's A operands: rows wm*64 + mt*32 + j32, chunk 4h + s
+    v4i aop[2][4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int n = n0 + wn * 64 + nt * 32 + j32;
-      uint4 wv = make_uint4(0, 0, 0, 0);
-      if (n < N) wv = *(const uint4*)(W + (size_t)n * wstride + (kb >> 2) + 16 * h);
-      const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+    for (int mt = 0; mt < 2; ++mt) {
+      const int r = wm * 64 + mt * 32 + j32;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint32_t pw = CANON ? w4[s] : canon_codes(w4[s]);
-        bop[nt][s][0] = (int)(pw & 0x03030303u);
-        bop[nt][s][1] = (int)((pw >> 2) & 0x03030303u);
-        bop[nt][s][2] = (int)((pw >> 4) & 0x03030303u);
-        bop[nt][s][3] = (int)((pw >> 6) & 0x03030303u);
+      for (int sub = 0; sub < 4; ++sub) {
+        const int pos = (4 * h + sub) ^ (r & 7);
+        aop[mt][sub] = *(const v4i*)(cur + r * GBK + 16 * pos);
       }
     }
+    {
+      // the next stage (unconditionally, so that no wait below has to cover
+      // both paths: after the last stage this reloads the last one into the
+      // buffer nobody reads any more)
+      const int kn = min(kb + GBK, K - GBK);
+      stage_a(kn, (st + 1) & 1);
+      stage_b(kn, bnext);
+    }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int sub = 0; sub < 4; ++sub) {
+      v4i bop[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int i = wm * 64 + mt * 32 + j32;
-        const v4i aop = *(const v4i*)(sA + i * GLDA + 64 * h + 16 * s);
+      for (int nt = 0; nt < 2; ++nt) {
+        const uint32_t w4[4] = {bcur[nt].x, bcur[nt].y, bcur[nt].z, bcur[nt].w};
+        const uint32_t pw = CANON ? w4[sub] : canon_codes(w4[sub]);
+        bop[nt][0] = (int)(pw & 0x03030303u);
+        bop[nt][1] = (int)((pw >> 2) & 0x03030303u);
+        bop[nt][2] = (int)((pw >> 4) & 0x03030303u);
+        bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[nt][s], acc[mt][nt], 0, 0, 0);
-      }
+          acc[mt][nt] =
+              __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[mt][sub], bop[nt], acc[mt][nt], 0, 0, 0);
     }
 
-    const bool slice_end = ((kb + GBK) % kSlice == 0) || (kb + GBK >= K);
-    if (slice_end) {
+    if (!I32 && (((kb + GBK) % kSlice == 0) || st + 1 == n_stages)) {
       const int slice = kb / kSlice;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int r = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          int sx = 0;
-          float inv = 0.0f;
-          if (r < M) {
-            sx = ((const int*)(act + (size_t)r * act_stride))[slice];
-            if (!I32) inv = inv_scale_of(scale_x[r], w_scale);
-          }
+        for (int g = 0; g < 4; ++g) {
+          // rows 8g + 4h + (0..3) of the tile: acc elements v = 4g .. 4g+3
+          const int rb = wm * 64 + mt * 32 + 8 * g + 4 * h;
+          const int4 sx4 = *(const int4*)&s_sx[slice][rb];
+          const float4 in4 = *(const float4*)&s_inv[rb];
+          const int sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+          const float inv[4] = {in4.x, in4.y, in4.z, in4.w};
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const int t = acc[mt][nt][v] - sx;
-            if (I32)
-              o[mt][nt][v] = __int_as_float(__float_as_int(o[mt][nt][v]) + t);
-            else
-              o[mt][nt][v] = __fadd_rn(o[mt][nt][v], __fmul_rn((float)t, inv));
-            acc[mt][nt][v] = 0;
-          }
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              const int v = 4 * g + e;
+              o[mt][nt][v] =
+                  __fadd_rn(o[mt][nt][v], __fmul_rn((float)(acc[mt][nt][v] - sx[e]), inv[e]));
+              acc[mt][nt][v] = 0;
+            }
         }
       }
     }
+    bcur[0] = bnext[0];
+    bcur[1] = bnext[1];
+    __syncthreads();
+  }
+
+  if (I32) {
+    // exact totals: x.code over all of K minus the sum of x over all slices
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rl = wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        int sx = 0;
+        for (int sl = 0; sl < n_slices; ++sl) sx += s_sx[sl][rl];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) o[mt][nt][v] = __int_as_float(acc[mt][nt][v] - sx);
+      }
   }
 
 #pragma unroll
