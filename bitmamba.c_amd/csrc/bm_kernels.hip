@@ -357,13 +357,13 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 //   of x is subtracted at each 1024-column slice boundary, where the int32
 //   totals are folded into fp32 in slice order.
 // ---------------------------------------------------------------------------
-constexpr int GBM = 128, GBN = 128, GBK = 128;
-constexpr int GMAX_SLICES = 16;  // K <= 16384
+constexpr int GBM = 128, GBN = 128, GBK = 128;  // GBK: the K granularity callers must meet
+constexpr int GMAX_SLICES = 16;                 // K <= 16384
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
-template <bool CANON, int MODE>
+template <bool CANON, int MODE, int BK>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act,
                                                  size_t act_stride,
                                                  const float* __restrict__ scale_x, int M,
@@ -371,8 +371,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
                                                  float w_scale, float* __restrict__ out,
                                                  int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][GBM * GBK];
-  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES + 1][GBM];  // [S] = total
+  constexpr int CH = BK / 16;         // 16-byte chunks per A row of a stage
+  constexpr int RPI = 1024 / BK;      // A rows per 1 KiB DMA instruction
+  constexpr int NI = GBM / RPI / 4;   // DMA instructions per wave per stage
+  constexpr int SUB = BK / 32;        // 32-deep MFMA steps per stage
+  constexpr int BU = BK / 128;        // 16-byte packed loads per lane per weight tile
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][GBM * BK];
+  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][GBM];
   __shared__ __attribute__((aligned(16))) float s_inv[GBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -381,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
   const size_t wstride = (size_t)(K >> 2);
   const size_t perm = act_perm_off(K);
   const int n_slices = slices_of(K);
-  const int n_stages = K / GBK;
+  const int n_stages = K / BK;
 
   // per-row slice sums of x and 1/(scale_x * w_scale)
   for (int i = tid; i < GBM * n_slices; i += 256) {
@@ -394,26 +399,29 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
     s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[row], w_scale);
   }
 
-  // LDS-DMA of one A stage: wave instruction i writes rows 8*(4i+wave) ..+8
-  // as 1 KiB; lane l lands at row l/8, chunk position l%8, and fetches the
-  // chunk (l%8) ^ (l/8) of that row.
+  // LDS-DMA of one A stage: wave instruction i writes rows RPI*(4i+wave)..
+  // as 1 KiB; lane l lands at row l/CH, chunk position l%CH, and fetches the
+  // chunk (l%CH) ^ (row % CH) of that row.
   auto stage_a = [&](int kb, int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rl = 8 * (4 * i + wave) + (lane >> 3);
+    for (int i = 0; i < NI; ++i) {
+      const int rl = RPI * (4 * i + wave) + lane / CH;
       const int row = min(m0 + rl, M - 1);
-      const int chunk = (lane & 7) ^ (lane >> 3);
+      const int chunk = (lane % CH) ^ (rl % CH);
       const uint8_t* src = act + (size_t)row * act_stride + perm + kb + 16 * chunk;
       __builtin_amdgcn_global_load_lds((glb_void_t*)src,
                                        (lds_void_t*)(sA[buf] + 1024 * (4 * i + wave)), 16, 0, 0);
     }
   };
-  // packed bytes of the wave's two 32-column weight tiles for one stage
-  auto stage_b = [&](int kb, uint4 (&bw)[2]) {
+  // packed bytes of the wave's two 32-column weight tiles for one stage:
+  // lane half h holds columns kb + (BK/2)h .. +BK/2
+  auto stage_b = [&](int kb, uint4 (&bw)[2][BU]) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int n = min(n0 + wn * 64 + nt * 32 + j32, N - 1);
-      bw[nt] = *(const uint4*)(W + (size_t)n * wstride + (kb >> 2) + 16 * h);
+#pragma unroll
+      for (int u = 0; u < BU; ++u)
+        bw[nt][u] = *(const uint4*)(W + (size_t)n * wstride + (kb >> 2) + (BK / 8) * h + 16 * u);
     }
   };
 
@@ -429,54 +437,60 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
         o[a][b][v] = 0.0f;
       }
 
-  uint4 bcur[2], bnext[2];
+  uint4 bcur[2][BU], bnext[2][BU];
   stage_a(0, 0);
   stage_b(0, bcur);
   __syncthreads();
 
   for (int st = 0; st < n_stages; ++st) {
-    const int kb = st * GBK;
+    const int kb = st * BK;
     const uint8_t* __restrict__ cur = sA[st & 1];
-    // this stage's A operands: rows wm*64 + mt*32 + j32, chunk 4h + s
-    v4i aop[2][4];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int r = wm * 64 + mt * 32 + j32;
+    for (int s0 = 0; s0 < SUB; s0 += 4) {
+      // A operands of steps s0..s0+3: rows wm*64 + mt*32 + j32, chunk
+      // (SUB)h + s
+      v4i aop[2][4];
 #pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const int pos = (4 * h + sub) ^ (r & 7);
-        aop[mt][sub] = *(const v4i*)(cur + r * GBK + 16 * pos);
+      for (int mt = 0; mt < 2; ++mt) {
+        const int r = wm * 64 + mt * 32 + j32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int pos = (SUB * h + s0 + q) ^ (r % CH);
+          aop[mt][q] = *(const v4i*)(cur + r * BK + 16 * pos);
+        }
       }
-    }
-    {
-      // the next stage (unconditionally, so that no wait below has to cover
-      // both paths: after the last stage this reloads the last one into the
-      // buffer nobody reads any more)
-      const int kn = min(kb + GBK, K - GBK);
-      stage_a(kn, (st + 1) & 1);
-      stage_b(kn, bnext);
-    }
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-      v4i bop[2];
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const uint32_t w4[4] = {bcur[nt].x, bcur[nt].y, bcur[nt].z, bcur[nt].w};
-        const uint32_t pw = CANON ? w4[sub] : canon_codes(w4[sub]);
-        bop[nt][0] = (int)(pw & 0x03030303u);
-        bop[nt][1] = (int)((pw >> 2) & 0x03030303u);
-        bop[nt][2] = (int)((pw >> 4) & 0x03030303u);
-        bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
+      if (s0 == 0) {
+        // the next stage (unconditionally, so that no wait below has to
+        // cover both paths: after the last stage this reloads the last one
+        // into the buffer nobody reads any more)
+        const int kn = min(kb + BK, K - BK);
+        stage_a(kn, (st + 1) & 1);
+        stage_b(kn, bnext);
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int q = 0; q < 4; ++q) {
+        const int sub = s0 + q;
+        v4i bop[2];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] =
-              __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[mt][sub], bop[nt], acc[mt][nt], 0, 0, 0);
+        for (int nt = 0; nt < 2; ++nt) {
+          const uint4 b4 = bcur[nt][sub / 4];
+          const uint32_t w4[4] = {b4.x, b4.y, b4.z, b4.w};
+          const uint32_t pw = CANON ? w4[sub % 4] : canon_codes(w4[sub % 4]);
+          bop[nt][0] = (int)(pw & 0x03030303u);
+          bop[nt][1] = (int)((pw >> 2) & 0x03030303u);
+          bop[nt][2] = (int)((pw >> 4) & 0x03030303u);
+          bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            acc[mt][nt] =
+                __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[mt][q], bop[nt], acc[mt][nt], 0, 0, 0);
+      }
     }
 
-    if (!I32 && (((kb + GBK) % kSlice == 0) || st + 1 == n_stages)) {
+    if (!I32 && (((kb + BK) % kSlice == 0) || st + 1 == n_stages)) {
       const int slice = kb / kSlice;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
@@ -500,8 +514,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
         }
       }
     }
-    bcur[0] = bnext[0];
-    bcur[1] = bnext[1];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int u = 0; u < BU; ++u) bcur[nt][u] = bnext[nt][u];
     __syncthreads();
   }
 
@@ -610,8 +626,12 @@ template <bool CANON, int MODE>
 static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
                          int K, float w_scale, void* out, hipStream_t s) {
   dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
-  hipLaunchKernelGGL((k_gemm<CANON, MODE>), grid, dim3(256), 0, s, act, act_row_bytes(K), scale_x,
-                     M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+  if (K % 256 == 0)
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, 256>), grid, dim3(256), 0, s, act, act_row_bytes(K),
+                       scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+  else
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, 128>), grid, dim3(256), 0, s, act, act_row_bytes(K),
+                       scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
   return hipGetLastError();
 }
 
