@@ -342,28 +342,46 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 // Prefill / batched GEMM on int8 MFMA (v_mfma_i32_32x32x32_i8).
 //   block 256 threads = 2x2 waves, tile 128(M) x 128(N), each wave 64 x 64
 //   (2 x 2 MFMA tiles); K in stages of 128.
-//   A (permuted int8 activations): each stage is streamed into one of two
-//   LDS buffers by LDS-DMA loads (16 bytes per lane, 1 KiB per wave
-//   instruction), its 16-byte chunks XOR-swizzled by row so the operand
-//   reads of 8 consecutive rows hit 8 different bank groups.  The next
-//   stage is issued right after the current one's operands are in
-//   registers, so one barrier per stage suffices.
-//   B: decoded from the packed bytes straight into operand registers: a
-//   16-byte load gives a lane 64 columns of one weight row, its operand for
-//   the stage's four 32-deep steps; the next stage's bytes are loaded while
-//   the current stage runs.
+//   Each stage (A: 128 rows x 128 permuted int8 activations; B: 128 weight
+//   rows x 32 packed bytes) is loaded into registers two stages ahead and
+//   written to one of two LDS buffers one stage ahead, so a load has two
+//   stages of MFMA work to arrive in; one barrier per stage.  LDS serves a
+//   16-byte read for 16 lanes per cycle from 64 banks: A's 16-byte chunks
+//   are XOR-swizzled by row/2 and B's two 16-byte halves by row/8, so the
+//   operand reads of 16 consecutive rows hit 16 different bank groups.
+//   B operands are decoded in registers: a lane's 16 packed bytes of one
+//   weight row are its operand for the stage's four 32-deep steps.
 //   Lane (j = lane%32, h = lane/32) covers columns kb + 64h + 16s.. in step
 //   s, for A and B alike.  Codes are used as is (0, 1, 2) and the slice sum
 //   of x is subtracted at each 1024-column slice boundary, where the int32
 //   totals are folded into fp32 in slice order.
 // ---------------------------------------------------------------------------
-constexpr int GBM = 128, GBN = 128, GBK = 128;  // GBK: the K granularity callers must meet
-constexpr int GMAX_SLICES = 16;                 // K <= 16384
+constexpr int GBM = 128, GBN = 128, GBK = 128;
+constexpr int GMAX_SLICES = 16;  // K <= 16384
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
+// Output tile of a block.  Workgroups go to the 8 XCDs round robin
+// (block b on XCD b % 8), each XCD with its own L2: every XCD is given one
+// contiguous run of tiles, walked in groups of 8 tile rows so that the
+// blocks resident at once share their A rows and weight columns in L2.
+__device__ __forceinline__ void gemm_tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int nb = tiles_m * tiles_n;
+  const int xcd = b % 8, local = b / 8;
+  const int per = nb / 8, extra = nb % 8;
+  const int t = xcd * per + min(xcd, extra) + local;
+  constexpr int G = 8;
+  const int g = t / (G * tiles_n);
+  const int rows = min(G, tiles_m - g * G);
+  const int r = t - g * G * tiles_n;
+  tm = g * G + r % rows;
+  tn = r / rows;
+}
 
-template <bool CANON, int MODE, int BK>
+struct GemmStage {
+  v4i a[4];  // 4 A chunks of this thread
+  v4i b;     // 1 B chunk of this thread
+};
+
+template <bool CANON, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act,
                                                  size_t act_stride,
                                                  const float* __restrict__ scale_x, int M,
@@ -371,22 +389,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
                                                  float w_scale, float* __restrict__ out,
                                                  int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
-  constexpr int CH = BK / 16;         // 16-byte chunks per A row of a stage
-  constexpr int RPI = 1024 / BK;      // A rows per 1 KiB DMA instruction
-  constexpr int NI = GBM / RPI / 4;   // DMA instructions per wave per stage
-  constexpr int SUB = BK / 32;        // 32-deep MFMA steps per stage
-  constexpr int BU = BK / 128;        // 16-byte packed loads per lane per weight tile
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][GBM * BK];
+  constexpr int BB = GBK / 4;  // packed bytes per weight row per stage
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][GBM * GBK];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2][GBN * BB];
   __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][GBM];
   __shared__ __attribute__((aligned(16))) float s_inv[GBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int j32 = lane & 31, h = lane >> 5;
-  const int m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
+  int tm, tn;
+  gemm_tile_of(blockIdx.x, (M + GBM - 1) / GBM, (N + GBN - 1) / GBN, tm, tn);
+  const int m0 = tm * GBM, n0 = tn * GBN;
   const size_t wstride = (size_t)(K >> 2);
   const size_t perm = act_perm_off(K);
   const int n_slices = slices_of(K);
-  const int n_stages = K / BK;
+  const int n_stages = K / GBK;
 
   // per-row slice sums of x and 1/(scale_x * w_scale)
   for (int i = tid; i < GBM * n_slices; i += 256) {
@@ -399,30 +416,29 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
     s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[row], w_scale);
   }
 
-  // LDS-DMA of one A stage: wave instruction i writes rows RPI*(4i+wave)..
-  // as 1 KiB; lane l lands at row l/CH, chunk position l%CH, and fetches the
-  // chunk (l%CH) ^ (row % CH) of that row.
-  auto stage_a = [&](int kb, int buf) {
+  // global -> registers: thread t loads A chunks g = t + 256i (row g/8,
+  // chunk g%8) and B chunk t (weight row t/2, half t%2).  Rows past M / N
+  // reread the last one; stages past K reread the last stage.
+  auto load_stage = [&](int st, GemmStage& r) __attribute__((always_inline)) {
+    const int kb = min(st, n_stages - 1) * GBK;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int rl = RPI * (4 * i + wave) + lane / CH;
-      const int row = min(m0 + rl, M - 1);
-      const int chunk = (lane % CH) ^ (rl % CH);
-      const uint8_t* src = act + (size_t)row * act_stride + perm + kb + 16 * chunk;
-      __builtin_amdgcn_global_load_lds((glb_void_t*)src,
-                                       (lds_void_t*)(sA[buf] + 1024 * (4 * i + wave)), 16, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      const int g = tid + 256 * i;
+      const int row = min(m0 + (g >> 3), M - 1);
+      r.a[i] = *(const v4i*)(act + (size_t)row * act_stride + perm + kb + 16 * (g & 7));
     }
+    const int n = min(n0 + (tid >> 1), N - 1);
+    r.b = *(const v4i*)(W + (size_t)n * wstride + (kb >> 2) + 16 * (tid & 1));
   };
-  // packed bytes of the wave's two 32-column weight tiles for one stage:
-  // lane half h holds columns kb + (BK/2)h .. +BK/2
-  auto stage_b = [&](int kb, uint4 (&bw)[2][BU]) {
+  auto store_stage = [&](int buf, const GemmStage& r) __attribute__((always_inline)) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int n = min(n0 + wn * 64 + nt * 32 + j32, N - 1);
-#pragma unroll
-      for (int u = 0; u < BU; ++u)
-        bw[nt][u] = *(const uint4*)(W + (size_t)n * wstride + (kb >> 2) + (BK / 8) * h + 16 * u);
+    for (int i = 0; i < 4; ++i) {
+      const int g = tid + 256 * i;
+      const int row = g >> 3;
+      *(v4i*)(sA[buf] + row * GBK + 16 * ((g & 7) ^ ((row >> 1) & 7))) = r.a[i];
     }
+    const int col = tid >> 1;
+    *(v4i*)(sB[buf] + col * BB + 16 * ((tid & 1) ^ ((col >> 3) & 1))) = r.b;
   };
 
   v16i acc[2][2];
@@ -437,60 +453,47 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
         o[a][b][v] = 0.0f;
       }
 
-  uint4 bcur[2][BU], bnext[2][BU];
-  stage_a(0, 0);
-  stage_b(0, bcur);
-  __syncthreads();
-
-  for (int st = 0; st < n_stages; ++st) {
-    const int kb = st * BK;
-    const uint8_t* __restrict__ cur = sA[st & 1];
+  // one stage: X holds stage st+1 (in flight), Y is free and receives st+2
+  auto body = [&](int st, GemmStage& X, GemmStage& Y) __attribute__((always_inline)) {
+    const uint8_t* __restrict__ cA = sA[st & 1];
+    const uint8_t* __restrict__ cB = sB[st & 1];
+    v4i aop[2][4];
 #pragma unroll
-    for (int s0 = 0; s0 < SUB; s0 += 4) {
-      // A operands of steps s0..s0+3: rows wm*64 + mt*32 + j32, chunk
-      // (SUB)h + s
-      v4i aop[2][4];
+    for (int mt = 0; mt < 2; ++mt) {
+      const int r = wm * 64 + mt * 32 + j32;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int r = wm * 64 + mt * 32 + j32;
+      for (int q = 0; q < 4; ++q)
+        aop[mt][q] = *(const v4i*)(cA + r * GBK + 16 * ((4 * h + q) ^ ((r >> 1) & 7)));
+    }
+    uint4 bw[2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int pos = (SUB * h + s0 + q) ^ (r % CH);
-          aop[mt][q] = *(const v4i*)(cur + r * BK + 16 * pos);
-        }
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = wn * 64 + nt * 32 + j32;
+      bw[nt] = *(const uint4*)(cB + col * BB + 16 * (h ^ ((col >> 3) & 1)));
+    }
+    load_stage(st + 2, Y);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v4i bop[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const uint32_t w4[4] = {bw[nt].x, bw[nt].y, bw[nt].z, bw[nt].w};
+        const uint32_t pw = CANON ? w4[q] : canon_codes(w4[q]);
+        bop[nt][0] = (int)(pw & 0x03030303u);
+        bop[nt][1] = (int)((pw >> 2) & 0x03030303u);
+        bop[nt][2] = (int)((pw >> 4) & 0x03030303u);
+        bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
       }
-      if (s0 == 0) {
-        // the next stage (unconditionally, so that no wait below has to
-        // cover both paths: after the last stage this reloads the last one
-        // into the buffer nobody reads any more)
-        const int kn = min(kb + BK, K - BK);
-        stage_a(kn, (st + 1) & 1);
-        stage_b(kn, bnext);
-      }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int sub = s0 + q;
-        v4i bop[2];
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const uint4 b4 = bcur[nt][sub / 4];
-          const uint32_t w4[4] = {b4.x, b4.y, b4.z, b4.w};
-          const uint32_t pw = CANON ? w4[sub % 4] : canon_codes(w4[sub % 4]);
-          bop[nt][0] = (int)(pw & 0x03030303u);
-          bop[nt][1] = (int)((pw >> 2) & 0x03030303u);
-          bop[nt][2] = (int)((pw >> 4) & 0x03030303u);
-          bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-            acc[mt][nt] =
-                __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[mt][q], bop[nt], acc[mt][nt], 0, 0, 0);
-      }
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] =
+              __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[mt][q], bop[nt], acc[mt][nt], 0, 0, 0);
     }
 
-    if (!I32 && (((kb + BK) % kSlice == 0) || st + 1 == n_stages)) {
+    const int kb = st * GBK;
+    if (!I32 && (((kb + GBK) % kSlice == 0) || st + 1 == n_stages)) {
       const int slice = kb / kSlice;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
@@ -514,12 +517,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ act
         }
       }
     }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int u = 0; u < BU; ++u) bcur[nt][u] = bnext[nt][u];
+    store_stage((st + 1) & 1, X);  // the buffer stage st-1 used
     __syncthreads();
+  };
+
+  GemmStage R0, R1;
+  load_stage(0, R0);
+  load_stage(1, R1);
+  store_stage(0, R0);
+  __syncthreads();
+  // two stages per turn so that each register set keeps its registers (no
+  // mid-turn exit: a merge there makes the loop head wait for every load)
+  int st = 0;
+  for (; st + 2 <= n_stages; st += 2) {
+    body(st, R1, R0);
+    body(st + 1, R0, R1);
   }
+  if (st < n_stages) body(st, R1, R0);
 
   if (I32) {
     // exact totals: x.code over all of K minus the sum of x over all slices
@@ -625,13 +639,9 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
 template <bool CANON, int MODE>
 static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
                          int K, float w_scale, void* out, hipStream_t s) {
-  dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM);
-  if (K % 256 == 0)
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 256>), grid, dim3(256), 0, s, act, act_row_bytes(K),
-                       scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
-  else
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 128>), grid, dim3(256), 0, s, act, act_row_bytes(K),
-                       scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+  const dim3 grid(((N + GBN - 1) / GBN) * ((M + GBM - 1) / GBM));
+  hipLaunchKernelGGL((k_gemm<CANON, MODE>), grid, dim3(256), 0, s, act, act_row_bytes(K), scale_x,
+                     M, W, N, K, w_scale, (float*)out, (int32_t*)out);
   return hipGetLastError();
 }
 

@@ -47,11 +47,13 @@ struct Backend {
   bool ready = false;
   int device = 0;
   hipStream_t stream = nullptr;
-  // weights and float vectors by host address
+  // weights and float vectors of registered model images, by host address
+  // (an image registered with bm_hip_set_mmap must not change afterwards)
   std::unordered_map<const void*, Registered> packed;
   std::unordered_map<const void*, Registered> floats;
-  // grow-on-demand device scratch for the host-pointer entry points
-  DevBuf d_x, d_out, d_norm, d_q, d_act, d_scale;
+  // grow-on-demand device scratch for the host-pointer entry points; d_w
+  // and d_g receive tensors that belong to no registered image, per call
+  DevBuf d_x, d_out, d_norm, d_q, d_act, d_scale, d_w, d_g;
   // pinned host staging
   DevBuf h_stage;
 };
@@ -125,6 +127,30 @@ const uint8_t* register_packed(Backend& b, const uint8_t* host, size_t bytes) {
   return (const uint8_t*)d;
 }
 
+// Device copy of a packed tensor for one call: the registered copy when the
+// tensor belongs to a registered image, else a fresh upload into d_w (host
+// memory outside an image may be reused for other data at any time, so it
+// is never cached).
+const uint8_t* packed_for_call(Backend& b, const uint8_t* host, size_t bytes) {
+  auto it = b.packed.find(host);
+  if (it != b.packed.end() && it->second.bytes >= bytes) return (const uint8_t*)it->second.dev;
+  if (!ensure_dev(b.d_w, bytes ? bytes : 1)) return nullptr;
+  BM_HIP_CHECK_RET(hipMemcpyAsync(b.d_w.ptr, host, bytes, hipMemcpyHostToDevice, b.stream),
+                   nullptr);
+  BM_HIP_CHECK_RET(bm::launch_canonicalize((uint8_t*)b.d_w.ptr, bytes, b.stream), nullptr);
+  BM_HIP_CHECK_RET(hipStreamSynchronize(b.stream), nullptr);
+  return (const uint8_t*)b.d_w.ptr;
+}
+
+const float* floats_for_call(Backend& b, const float* host, size_t count) {
+  const size_t bytes = count * sizeof(float);
+  auto it = b.floats.find(host);
+  if (it != b.floats.end() && it->second.bytes >= bytes) return (const float*)it->second.dev;
+  if (!ensure_dev(b.d_g, bytes ? bytes : 4)) return nullptr;
+  BM_HIP_CHECK_RET(hipMemcpy(b.d_g.ptr, host, bytes, hipMemcpyHostToDevice), nullptr);
+  return (const float*)b.d_g.ptr;
+}
+
 const float* register_floats(Backend& b, const float* host, size_t count) {
   const size_t bytes = count * sizeof(float);
   auto it = b.floats.find(host);
@@ -162,8 +188,8 @@ void host_bitlinear(const float* x, int M, int n, const uint8_t* packed, int row
   if (!init_locked(b)) die("init");
   if (M <= 0) return;
   const size_t wbytes = (size_t)rows * (size_t)((cols + 3) / 4);
-  const uint8_t* dW = register_packed(b, packed, wbytes);
-  const float* dG = register_floats(b, norm_w, (size_t)n);
+  const uint8_t* dW = packed_for_call(b, packed, wbytes);
+  const float* dG = floats_for_call(b, norm_w, (size_t)n);
   if (!dW || !dG) die("weight upload");
 
   const size_t xbytes = (size_t)M * n * sizeof(float);
@@ -265,7 +291,7 @@ extern "C" void bm_hip_cleanup(void) {
   for (auto& kv : b.floats) (void)hipFree(kv.second.dev);
   b.packed.clear();
   b.floats.clear();
-  for (DevBuf* d : {&b.d_x, &b.d_out, &b.d_norm, &b.d_q, &b.d_act, &b.d_scale}) {
+  for (DevBuf* d : {&b.d_x, &b.d_out, &b.d_norm, &b.d_q, &b.d_act, &b.d_scale, &b.d_w, &b.d_g}) {
     if (d->ptr) (void)hipFree(d->ptr);
     *d = DevBuf{};
   }
@@ -283,7 +309,7 @@ extern "C" float hip_rms_norm(const float* x, int size, const float* weight, flo
   Backend& b = B();
   std::lock_guard<std::mutex> lk(b.mu);
   if (!init_locked(b)) die("init");
-  const float* dG = register_floats(b, weight, (size_t)size);
+  const float* dG = floats_for_call(b, weight, (size_t)size);
   const size_t xbytes = (size_t)size * sizeof(float);
   if (!dG || !ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_norm, xbytes) ||
       !ensure_dev(b.d_scale, 16) || !ensure_pinned(b.h_stage, xbytes + 16))

@@ -58,8 +58,9 @@ bool bm_hip_available(void);
  * tensor is copied once into its own 256-byte-aligned device buffer with
  * the 2-bit code 11 rewritten to 10 (same value, src/quantization.c:27-31),
  * and every float tensor is copied too; hip_* calls then find them by host
- * pointer.  Host tensors that were never registered are uploaded on first
- * use.  Registered host memory must not change afterwards. */
+ * pointer.  Tensors outside a registered image are uploaded on every call
+ * (their host memory may be reused for other data).  Registered host memory
+ * must not change afterwards. */
 bool bm_hip_set_mmap(const void *base, size_t size);
 /* bm_metal_cleanup (src/metal/bm_metal.h:45) */
 void bm_hip_cleanup(void);

@@ -233,6 +233,34 @@ def test_dropin_cfg1_golden(hip):
     np.testing.assert_array_equal(xq[:K], z["x_quant"][0])
 
 
+def test_dropin_reused_host_buffers(hip):
+    """The same host arrays refilled with other weights and norm between
+    calls (as when an allocator reuses freed memory): every call must see the
+    current contents, checked against the oracle."""
+    K, N = 2048, 300
+    packed = np.empty((N, K // 4), np.uint8)
+    g = np.empty(K, np.float32)
+    O = native.oracle()
+    for seed in (21, 22, 23):
+        note("drop-in reused buffers seed=%d" % seed)
+        r = rnd(seed)
+        packed[:] = r.integers(0, 256, packed.shape, dtype=np.uint8)
+        g[:] = r.standard_normal(K).astype(np.float32)
+        x = r.standard_normal(K).astype(np.float32)
+        w = bh.make_tensor(packed, N, K, 0.03)
+        nw = bh.make_tensor(data=g)
+        out = np.empty(N, np.float32)
+        xn = np.empty(K, np.float32)
+        xq = np.zeros(K + 32, np.int8)
+        hip.hip_bitlinear_forward(ptr(x), K, C.byref(w), C.byref(nw), ptr(out), ptr(xn), ptr(xq))
+        ref = np.empty(N, np.float32)
+        rxn = np.empty(K, np.float32)
+        rxq = np.zeros(K + 32, np.int8)
+        O.orc_bitlinear_forward(ptr(x), K, ptr(packed), N, K, C.c_float(0.03), ptr(g), ptr(ref),
+                                ptr(rxn), ptr(rxq))
+        same_bits(out, ref, "out seed %d" % seed)
+
+
 def test_dropin_batch_golden_shapes(hip):
     z = np.load(os.path.join(GOLD, "bitlinear_shapes.npz"))
     for key in sorted(k[4:] for k in z.files if k.startswith("out_")):
