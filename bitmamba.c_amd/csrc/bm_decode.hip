@@ -450,6 +450,125 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
 }
 
 // ---------------------------------------------------------------------------
+// in_proj + SSM step in one kernel.  Block (head h, channel group q) owns
+// kCB channels of the head: it computes their z and x rows and the head's
+// B, C, dt rows (each block of a head recomputes these three), then runs the
+// SSM step of its channels (src/kernel.c:34-70) from the values in LDS.
+// The per-head row layout of the weights is [z (hd) | x (hd) | B | C | dt].
+// ---------------------------------------------------------------------------
+constexpr int kCB = 16;              // channels per block
+constexpr int kRowsCB = 2 * kCB + 3;  // weight rows per block
+
+struct SsmArgs {
+  const float* dt_bias;
+  const float* A;
+  const float* cw;  // [4][di]
+  const float* cb;
+  float* cs;        // [3][di] ring
+  float* ssm;
+  const float* D;
+  float* y;
+  const int* ctl;
+  int hd, di;
+};
+
+template <int T, int P, int NPF, int C>
+__global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x, int K,
+                                                    const float* __restrict__ gamma,
+                                                    const uint8_t* __restrict__ W, float w_scale,
+                                                    SsmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ float s_proj[kRowsCB];
+  constexpr int RPW = 64 / T;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int u = lane % T, sub = lane / T, unit_base = sub * T;
+  const int hd = a.hd, groups_per_head = hd / kCB;
+  const int h = blockIdx.x / groups_per_head, q = blockIdx.x % groups_per_head;
+  const size_t wstride = (size_t)(K >> 2);
+  const int chunks = K >> 6;
+  const int n_groups = (kRowsCB + RPW - 1) / RPW;
+  // weight row of local row r
+  auto wrow = [&](int r) {
+    const int base = h * (2 * hd + 3);
+    if (r < kCB) return base + q * kCB + r;
+    if (r < 2 * kCB) return base + hd + q * kCB + (r - kCB);
+    return base + 2 * hd + (r - 2 * kCB);
+  };
+
+  float4 sx[C], sg[C];
+  stage_load<C>(sx, x, K);
+  stage_load<C>(sg, gamma, K);
+
+  uint4 wv[NPF][P];
+#pragma unroll
+  for (int it = 0; it < NPF; ++it) {
+    const int grp = wave + 4 * it;
+    const int r = min(grp * RPW + sub, kRowsCB - 1);
+    const size_t roff = (size_t)wrow(r) * wstride;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = min(p * T + u, chunks - 1);
+      wv[it][p] = load_stream16(W + roff + 16 * j);
+    }
+  }
+
+  // SSM inputs of this thread's channel (threads 0..kCB-1), fetched while the
+  // prologue runs
+  const int c = tid < kCB ? tid : 0;
+  const int idx = h * hd + q * kCB + c;
+  const int pos = a.ctl[CTL_POS];
+  const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
+  const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
+  const float tap0 = a.cs[(size_t)pos * a.di + idx];
+  const float tap1 = a.cs[(size_t)t1 * a.di + idx];
+  const float tap2 = a.cs[(size_t)t2 * a.di + idx];
+  const float cw0 = a.cw[idx], cw1 = a.cw[a.di + idx], cw2 = a.cw[2 * a.di + idx];
+  const float cw3 = a.cw[3 * a.di + idx], cbias = a.cb[idx], st0 = a.ssm[idx], Dc = a.D[idx];
+  const float dtb = a.dt_bias[h], Ah = a.A[h];
+
+  const Lds l = lds_carve(lds, K);
+  const float rms = pro_rms<C>(sx, K, l);
+  const float scale_x = pro_quant<C>(sx, sg, rms, K, l);
+  const float inv = inv_scale_of(scale_x, w_scale);
+  uint32_t xa[P][16];
+  int xsl[P];
+  load_lane_act<P, T>(l, K, u, xa, xsl);
+
+#pragma unroll
+  for (int it = 0; it < NPF; ++it) {
+    const int grp = wave + 4 * it;
+    if (grp < n_groups) {  // uniform per wave
+      float o = 0.0f;
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        o = row_finish<T>(dot64(wv[it][p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+      const int r = grp * RPW + sub;
+      if (u == 0 && r < kRowsCB) s_proj[r] = o;
+    }
+  }
+  __syncthreads();
+
+  if (tid < kCB) {
+    // scalar_ssm_inner for channel idx (src/kernel.c:34-70)
+    const float dt_val = softplus_r(__fadd_rn(s_proj[2 * kCB + 2], dtb));
+    const float decay = libm::expf_glibc(__fmul_rn(Ah, dt_val));
+    const float Bdt = __fmul_rn(s_proj[2 * kCB], dt_val);
+    const float C_val = s_proj[2 * kCB + 1];
+    const float xin = s_proj[kCB + c];
+    float conv = __fadd_rn(cbias, __fmul_rn(tap0, cw0));
+    conv = __fadd_rn(conv, __fmul_rn(tap1, cw1));
+    conv = __fadd_rn(conv, __fmul_rn(tap2, cw2));
+    conv = __fadd_rn(conv, __fmul_rn(xin, cw3));
+    a.cs[(size_t)pos * a.di + idx] = xin;  // the oldest tap is overwritten
+    const float xact = silu_r(conv);
+    const float st = __fadd_rn(__fmul_rn(st0, decay), __fmul_rn(xact, Bdt));
+    a.ssm[idx] = st;
+    a.y[idx] =
+        __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xact, Dc)), silu_r(s_proj[c]));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // SSM step, one block per head, one thread per channel.  proj holds the
 // in_proj outputs per head as [z (hd) | x (hd) | B | C | dt].
 // ---------------------------------------------------------------------------
@@ -591,6 +710,32 @@ hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
                           float w_scale, float* x, hipStream_t s) {
   return rows_t<2, false, 1, false>(y, K, nullptr, gamma, W, N, w_scale, x, nullptr, nullptr, s);
+}
+
+bool inproj_ssm_fits(int K, int hd) { return K % 64 == 0 && K <= 8192 && hd % kCB == 0; }
+
+// in_proj + SSM for every head: y (and the states) updated in one launch
+hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
+                             float w_scale, int nh, int hd, const float* dt_bias, const float* A,
+                             const float* cw, const float* cb, float* cs, float* ssm,
+                             const float* D, float* y, const int* ctl, hipStream_t s) {
+  if (!inproj_ssm_fits(K, hd)) return hipErrorInvalidValue;
+  const SsmArgs args{dt_bias, A, cw, cb, cs, ssm, D, y, ctl, hd, nh * hd};
+  const dim3 grid(nh * (hd / kCB)), block(256);
+  const size_t lds = lds_bytes(K);
+  if (K <= 1024)
+    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1>), grid, block, lds, s, x, K, gamma, W, w_scale,
+                       args);
+  else if (K <= 2048)
+    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2>), grid, block, lds, s, x, K, gamma, W, w_scale,
+                       args);
+  else if (K <= 4096)
+    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4>), grid, block, lds, s, x, K, gamma, W, w_scale,
+                       args);
+  else
+    hipLaunchKernelGGL((k_inproj_ssm<64, 2, 9, 8>), grid, block, lds, s, x, K, gamma, W, w_scale,
+                       args);
+  return hipGetLastError();
 }
 
 hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,

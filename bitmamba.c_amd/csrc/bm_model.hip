@@ -183,6 +183,11 @@ hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_
                          float w_scale, float* proj, hipStream_t s);
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
                           float w_scale, float* x, hipStream_t s);
+bool inproj_ssm_fits(int K, int hd);
+hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
+                             float w_scale, int nh, int hd, const float* dt_bias, const float* A,
+                             const float* cw, const float* cb, float* cs, float* ssm,
+                             const float* D, float* y, const int* ctl, hipStream_t s);
 hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
                             const float* A, const float* cw, const float* cb, float* cs,
                             float* ssm, const float* D, float* y, const int* ctl, hipStream_t s);
@@ -286,9 +291,16 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
     float* cs = m->conv_state + (size_t)l * 3 * di;
     float* ss = m->ssm_state + (size_t)l * di;
     // block_step, unfused branch (src/block.c:361-371), then the residual
-    MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj, s));
-    MCHECK(bm::launch_ssm_heads(m->proj, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b,
-                                cs, ss, Ly.D, m->y, m->ctl, s));
+    if (bm::inproj_ssm_fits(dm, m->hd)) {
+      MCHECK(bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
+                                   Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
+                                   m->ctl, s));
+    } else {
+      MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
+                               s));
+      MCHECK(bm::launch_ssm_heads(m->proj, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt,
+                                  Ly.conv_b, cs, ss, Ly.D, m->y, m->ctl, s));
+    }
     MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s));
   }
   const bool fused_pick = penalty == 1.0f;  // x / 1.0f == x * 1.0f == x
