@@ -260,6 +260,119 @@ __device__ float pro_quant(const float4 (&xv)[C], const float4 (&gv)[C], float r
 }
 
 // ---------------------------------------------------------------------------
+// Prologue for K = 1024 * G (G in {1, 2, 4}): thread t owns the 16-column
+// group t (t < K/16) in registers for the whole prologue; the squares go
+// through LDS once to reach the chain layout, wave 0 runs the chains, and
+// the int8 values are packed straight from registers.  Group t lies in
+// slice t/64 = the thread's wave.  Returns scale_x.
+//   PRENORM: x first becomes (x * rms(x)) * g_pre (the final norm).
+// ---------------------------------------------------------------------------
+template <int G>
+__device__ __forceinline__ void put_squares(const float4 (&v)[4], bool has, const Lds& l) {
+  constexpr int E = 1024 * G / 64;
+  if (!has) return;
+  // column 16t + 4k + j is element 4t + k of chain j (segments of E
+  // elements padded by 4 floats)
+  const int e = 4 * (int)threadIdx.x;
+  const int pe = e + 4 * (e / E);
+  *(float4*)&l.sq[pe] = make_float4(__fmul_rn(v[0].x, v[0].x), __fmul_rn(v[1].x, v[1].x),
+                                    __fmul_rn(v[2].x, v[2].x), __fmul_rn(v[3].x, v[3].x));
+  *(float4*)&l.sq[l.stride + pe] = make_float4(__fmul_rn(v[0].y, v[0].y), __fmul_rn(v[1].y, v[1].y),
+                                               __fmul_rn(v[2].y, v[2].y), __fmul_rn(v[3].y, v[3].y));
+  *(float4*)&l.sq[2 * l.stride + pe] =
+      make_float4(__fmul_rn(v[0].z, v[0].z), __fmul_rn(v[1].z, v[1].z), __fmul_rn(v[2].z, v[2].z),
+                  __fmul_rn(v[3].z, v[3].z));
+  *(float4*)&l.sq[3 * l.stride + pe] =
+      make_float4(__fmul_rn(v[0].w, v[0].w), __fmul_rn(v[1].w, v[1].w), __fmul_rn(v[2].w, v[2].w),
+                  __fmul_rn(v[3].w, v[3].w));
+}
+
+// rms = 1/sqrtf(sum/K + 1e-6f) from the squares in LDS; wave 0 runs the
+// chains, the result is broadcast through LDS (src/kernel.c:77-91)
+template <int G>
+__device__ __forceinline__ float chain_rms(const Lds& l) {
+  constexpr int K = 1024 * G, E = K / 64;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const float cs = chain_regs<E>(l.sq, l.stride, threadIdx.x);
+    const float s0 = lane_f32(cs, 15), s1 = lane_f32(cs, 31);
+    const float s2 = lane_f32(cs, 47), s3 = lane_f32(cs, 63);
+    if (threadIdx.x == 0) {
+      const float sum = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+      // sum / K with K a power of two: an exact scaling, rounded like the
+      // division
+      l.bc[0] = cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(sum, 1.0f / K), 1e-6f)));
+    }
+  }
+  __syncthreads();
+  return l.bc[0];
+}
+
+template <int G, bool PRENORM>
+__device__ float split_prologue(const float* __restrict__ x, const float* __restrict__ g_pre,
+                                const float* __restrict__ g, const Lds& l) {
+  constexpr int NG = 1024 * G / 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool has = tid < NG;
+  const int c4 = 4 * (has ? tid : 0);
+  float4 xv[4], gv[4], gp[PRENORM ? 4 : 1];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    xv[k] = ((const float4*)x)[c4 + k];
+    gv[k] = ((const float4*)g)[c4 + k];
+    if constexpr (PRENORM) gp[k] = ((const float4*)g_pre)[c4 + k];
+  }
+  put_squares<G>(xv, has, l);
+  float rms = chain_rms<G>(l);
+  if constexpr (PRENORM) {
+    // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xv[k] = scale4(xv[k], rms, gp[k]);
+    put_squares<G>(xv, has, l);
+    rms = chain_rms<G>(l);
+  }
+  // int8 quantization (src/kernel.c:93-128, 358-386)
+  float mx = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    xv[k] = scale4(xv[k], rms, gv[k]);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[k].x), fabsf(xv[k].y)),
+                         fmaxf(fabsf(xv[k].z), fabsf(xv[k].w))));
+  }
+  mx = wave_max_f32(has ? mx : 0.0f);
+  if (lane == 0) l.bc[8 + wave] = mx;
+  __syncthreads();
+  const float max_abs = fmaxf(fmaxf(l.bc[8], l.bc[9]), fmaxf(l.bc[10], l.bc[11]));
+  const float scale_x = cr_divf(127.0f, __fadd_rn(max_abs, 1e-5f));
+  int qsum = 0;
+  if (has) {
+    int q[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float vv[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[4 * k + j] = (int)(int8_t)q8_of(vv[j], scale_x);
+        qsum += q[4 * k + j];
+      }
+    }
+    uint32_t le = 0, lo = 0, he = 0, ho = 0;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      le |= (uint32_t)(q[2 * n] & 15) << (4 * n);
+      lo |= (uint32_t)(q[2 * n + 1] & 15) << (4 * n);
+      he |= (uint32_t)((q[2 * n] >> 4) & 15) << (4 * n);
+      ho |= (uint32_t)((q[2 * n + 1] >> 4) & 15) << (4 * n);
+    }
+    *(uint4*)(l.nib + 4 * tid) = make_uint4(le, lo, he, ho);
+  }
+  const int ssum = wave_sum_i32(qsum);  // the wave's 64 groups = slice `wave`
+  if (lane == 0 && wave < G) l.slices[wave] = ssum;
+  __syncthreads();
+  return scale_x;
+}
+
+// ---------------------------------------------------------------------------
 // GEMV pieces
 // ---------------------------------------------------------------------------
 
@@ -286,15 +399,18 @@ __device__ __forceinline__ int dot64(uint4 w, const uint32_t (&xa)[16]) {
 template <int T>
 __device__ __forceinline__ float row_finish(int part, int xs_slice, int p_index, int n_slices,
                                             float inv, float o, int unit_base) {
-  part += __shfl_xor(part, 8, 64);
-  part += __shfl_xor(part, 4, 64);
-  part += __shfl_xor(part, 2, 64);
-  part += __shfl_xor(part, 1, 64);
+  part = row_sum_i32(part);
   const float f = __fmul_rn((float)(part - xs_slice), inv);
+  if constexpr (T == 16) {
+    if (p_index < n_slices) o = __fadd_rn(o, f);
+  } else {
+    // the team's rows (16-lane slices) in order: rows unit_base/16 ..
+    const float r[4] = {lane_f32(f, 0), lane_f32(f, 16), lane_f32(f, 32), lane_f32(f, 48)};
 #pragma unroll
-  for (int q = 0; q < T / 16; ++q) {
-    const float fq = __shfl(f, unit_base + 16 * q, 64);
-    if (p_index * (T / 16) + q < n_slices) o = __fadd_rn(o, fq);
+    for (int q = 0; q < T / 16; ++q) {
+      const float fq = T == 64 ? r[q] : (unit_base == 0 ? r[q] : r[2 + q]);
+      if (p_index * (T / 16) + q < n_slices) o = __fadd_rn(o, fq);
+    }
   }
   return o;
 }
@@ -326,7 +442,7 @@ __device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32
 //   MODE:    0 store, 1 accumulate (residual)
 //   PICK:    each block also writes its first-max row (value, index)
 // ---------------------------------------------------------------------------
-template <int T, int P, int NPF, int C, bool PRENORM, int MODE, bool PICK>
+template <int T, int P, int NPF, int C, bool PRENORM, int MODE, bool PICK, bool WP>
 __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma_pre,
                                                     const float* __restrict__ gamma,
@@ -339,16 +455,19 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int u = lane % T, sub = lane / T, unit_base = sub * T;
   const int G = (N + RPW - 1) / RPW;
-  const int g0 = (int)((long long)blockIdx.x * G / gridDim.x);
-  const int g1 = (int)((long long)(blockIdx.x + 1) * G / gridDim.x);
+  const int per = G / (int)gridDim.x, extra = G % (int)gridDim.x, b = blockIdx.x;
+  const int g0 = b * per + min(b, extra);
+  const int g1 = g0 + per + (b < extra ? 1 : 0);
   const size_t wstride = (size_t)(K >> 2);
   const int chunks = K >> 6;
 
   // the input vectors first (the prologue waits for them), then the weights
-  float4 sx[C], sg[C], sg2[PRENORM ? C : 1];
-  stage_load<C>(sx, x, K);
-  stage_load<C>(sg, PRENORM ? gamma_pre : gamma, K);
-  if constexpr (PRENORM) stage_load<C>(sg2, gamma, K);
+  float4 sx[WP ? 1 : C], sg[WP ? 1 : C], sg2[PRENORM && !WP ? C : 1];
+  if constexpr (!WP) {
+    stage_load<C>(sx, x, K);
+    stage_load<C>(sg, PRENORM ? gamma_pre : gamma, K);
+    if constexpr (PRENORM) stage_load<C>(sg2, gamma, K);
+  }
 
   uint4 wv[NPF][P];
 #pragma unroll
@@ -365,16 +484,20 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   }
 
   const Lds l = lds_carve(lds, K);
-  float rms = pro_rms<C>(sx, K, l);
   float scale_x;
-  if constexpr (PRENORM) {
-    // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
-#pragma unroll
-    for (int i = 0; i < C; ++i) sx[i] = scale4(sx[i], rms, sg[i]);
-    rms = pro_rms<C>(sx, K, l);
-    scale_x = pro_quant<C>(sx, sg2, rms, K, l);
+  if constexpr (WP) {
+    scale_x = split_prologue<C, PRENORM>(x, gamma_pre, gamma, l);
   } else {
-    scale_x = pro_quant<C>(sx, sg, rms, K, l);
+    float rms = pro_rms<C>(sx, K, l);
+    if constexpr (PRENORM) {
+      // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
+#pragma unroll
+      for (int i = 0; i < C; ++i) sx[i] = scale4(sx[i], rms, sg[i]);
+      rms = pro_rms<C>(sx, K, l);
+      scale_x = pro_quant<C>(sx, sg2, rms, K, l);
+    } else {
+      scale_x = pro_quant<C>(sx, sg, rms, K, l);
+    }
   }
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
@@ -472,7 +595,7 @@ struct SsmArgs {
   int hd, di;
 };
 
-template <int T, int P, int NPF, int C>
+template <int T, int P, int NPF, int C, bool WP>
 __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma,
                                                     const uint8_t* __restrict__ W, float w_scale,
@@ -495,9 +618,11 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
     return base + 2 * hd + (r - 2 * kCB);
   };
 
-  float4 sx[C], sg[C];
-  stage_load<C>(sx, x, K);
-  stage_load<C>(sg, gamma, K);
+  float4 sx[WP ? 1 : C], sg[WP ? 1 : C];
+  if constexpr (!WP) {
+    stage_load<C>(sx, x, K);
+    stage_load<C>(sg, gamma, K);
+  }
 
   uint4 wv[NPF][P];
 #pragma unroll
@@ -527,8 +652,13 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   const float dtb = a.dt_bias[h], Ah = a.A[h];
 
   const Lds l = lds_carve(lds, K);
-  const float rms = pro_rms<C>(sx, K, l);
-  const float scale_x = pro_quant<C>(sx, sg, rms, K, l);
+  float scale_x;
+  if constexpr (WP) {
+    scale_x = split_prologue<C, false>(x, nullptr, gamma, l);
+  } else {
+    const float rms = pro_rms<C>(sx, K, l);
+    scale_x = pro_quant<C>(sx, sg, rms, K, l);
+  }
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
   int xsl[P];
@@ -682,18 +812,27 @@ static hipError_t rows_t(const float* x, int K, const float* gpre, const float* 
   const size_t lds = lds_bytes(K);
   const dim3 grid(rows_blocks<NPF>(N, K)), block(256);
   if (K % 64 != 0) return hipErrorInvalidValue;
-  if (K <= 1024)
-    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK>), grid, block, lds, s, x,
-                       K, gpre, g, W, N, w_scale, out, pv, pi);
+  if (K == 1024)
+    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true>), grid, block, lds,
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+  else if (K == 2048)
+    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true>), grid, block, lds,
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+  else if (K == 4096)
+    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, true>), grid, block, lds,
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+  else if (K <= 1024)
+    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, false>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
   else if (K <= 2048)
-    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK>), grid, block, lds, s, x,
-                       K, gpre, g, W, N, w_scale, out, pv, pi);
+    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, false>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
   else if (K <= 4096)
-    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK>), grid, block, lds, s, x,
-                       K, gpre, g, W, N, w_scale, out, pv, pi);
+    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, false>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
   else if (K <= 8192)
-    hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK>), grid, block, lds, s, x,
-                       K, gpre, g, W, N, w_scale, out, pv, pi);
+    hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK, false>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -723,18 +862,27 @@ hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const ui
   const SsmArgs args{dt_bias, A, cw, cb, cs, ssm, D, y, ctl, hd, nh * hd};
   const dim3 grid(nh * (hd / kCB)), block(256);
   const size_t lds = lds_bytes(K);
-  if (K <= 1024)
-    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       args);
+  if (K == 1024)
+    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, true>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
+  else if (K == 2048)
+    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, true>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
+  else if (K == 4096)
+    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, true>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
+  else if (K <= 1024)
+    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, false>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
   else if (K <= 2048)
-    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       args);
+    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, false>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
   else if (K <= 4096)
-    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       args);
+    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, false>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
   else
-    hipLaunchKernelGGL((k_inproj_ssm<64, 2, 9, 8>), grid, block, lds, s, x, K, gamma, W, w_scale,
-                       args);
+    hipLaunchKernelGGL((k_inproj_ssm<64, 2, 9, 8, false>), grid, block, lds, s, x, K, gamma, W,
+                       w_scale, args);
   return hipGetLastError();
 }
 

@@ -47,16 +47,47 @@ __device__ __forceinline__ void write_act_group(uint8_t* __restrict__ act_row, i
   *(uint4*)(act_row + act_perm_off(K) + 16 * (size_t)g) = make_uint4(pm[0], pm[1], pm[2], pm[3]);
 }
 
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane reductions on DPP (no LDS round trips).  All 64 lanes must be
+// active.  Within a 16-lane row: quad_perm [1,0,3,2] and [2,3,0,1] give
+// every lane its quad's value, row_half_mirror pairs the two quads of each
+// half row, row_mirror the two half rows.  Rows are then combined through
+// scalar reads of lanes 0, 16, 32, 48.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+
+// sum over the 16 lanes of each row, in every lane of the row
+__device__ __forceinline__ int row_sum_i32(int v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
   return v;
 }
 
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+__device__ __forceinline__ float row_max_f32(float v) {
+  v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
   return v;
+}
+
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// sum / max over the wave, in every lane
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v = row_sum_i32(v);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = row_max_f32(v);
+  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
 __device__ __forceinline__ float inv_scale_of(float scale_x, float w_scale) {
