@@ -16,6 +16,13 @@ Prints ONE JSON line.  Legs (all by default):
   prefill   int8-MFMA GEMM at M=2048: 2048->8512 and 4096->2048, TOP/s
   cpu       the reference's own AVX2 build (oracle/_ref) on the host cores:
             a bounded sample of the same decode workload
+  gemv1     the single K=1024 -> N=4384 BitLinear (uniform ternary, N(0,1)
+            input): device call time (warm, cache-resident), the host-pointer
+            drop-in call (PCIe included), and the reference's own CPU build
+            (AVX2 with the leg's thread count, scalar on 1 thread)
+  d255m     255M-shape greedy decode, 128 steps (tok/s, stream identity)
+  stress    int8-input ternary products at K = N = 8192, p(0) = 0.6, exact
+            int32 outputs: M = 1, 16 (weight GB/s, warm) and 4096 (TOP/s)
   copy      (on request only) a plain 512 MiB device copy: the calibration
             run for the HBM traffic counters
 The roofline's `traffic` (HBM bytes per launch of the GEMV) is read from
@@ -39,6 +46,8 @@ import bitmamba_hip as bh  # noqa: E402
 METRIC = "packed-weight GB/s + tok/s (1B-shape decode, bs=1); prefill ternary GEMM TOPS"
 CFG_1B = dict(vocab=50257, d_model=2048, n_layers=24, n_heads=64, dist=bh.SYNTH_P0_40,
               seed=1000, prompt=8)
+CFG_255M = dict(vocab=50257, d_model=1024, n_layers=24, n_heads=32, dist=bh.SYNTH_UNIFORM,
+                seed=255, prompt=8, steps=128)
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_k2048_traffic.txt")
 I8_PEAK_TOPS = 5000.0
@@ -91,6 +100,157 @@ def leg_decode(L, steps, warmup):
         n = min(len(ref), len(toks))
         match = toks[:n].tolist() == ref[:n]
     return wall, dev_ms, match
+
+
+def leg_d255m(L):
+    c = CFG_255M
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          c["dist"])
+    prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
+    m = bh.Model(blob)
+    del blob
+    m.generate(prompt, 4)                            # warm the step graph
+    m.reset()
+    toks, ms = m.generate(prompt, c["steps"])        # device time of the decode steps
+    m.free()
+    match = None
+    gold = os.path.join(ROOT, "tests", "golden", "stream_255m.json")
+    if os.path.exists(gold):
+        match = toks.tolist() == json.load(open(gold))["tokens"]
+    bpt = packed_bytes_per_token(c)
+    tok_s = c["steps"] / (ms * 1e-3)
+    return dict(tok_s=round(tok_s, 1), ms_per_step=round(ms / c["steps"], 4),
+                packed_weight_GBps=round(tok_s * bpt / 1e9, 1), packed_bytes_per_token=bpt,
+                tokens_match_reference=match, steps=c["steps"])
+
+
+def gemv1_inputs():
+    K, N = 1024, 4384
+    return (bh.synth_ternary(1, 1, N, K, bh.SYNTH_UNIFORM), bh.synth_normal(1, 2, (1, K), 1.0),
+            np.ones(K, np.float32), K, N, 0.02)
+
+
+def leg_gemv1(L, reps=200):
+    packed, x, g, K, N, scale = gemv1_inputs()
+    dW, dx, dg = (bh.DeviceBuffer.from_array(a) for a in (packed, x, g))
+    dout, dq, ds = bh.DeviceBuffer(4 * N), bh.DeviceBuffer(K), bh.DeviceBuffer(4)
+    da = bh.DeviceBuffer(L.bm_hip_act_bytes(1, K))
+    call = lambda: bh.check(L.bm_hip_bitlinear_dev(dx.ptr, 1, K, dg.ptr, dW.ptr, N, scale, 1,
+                                                   dout.ptr, dq.ptr, K, ds.ptr, da.ptr, None),
+                            "bitlinear")
+    for _ in range(5):
+        call()
+    ev = Events(L)
+    ev.start()
+    for _ in range(reps):
+        call()
+    dev_us = ev.stop_ms() * 1e3 / reps
+    for b in (dW, dx, dg, dout, dq, ds, da):
+        b.free()
+    # the drop-in entry with host buffers (PCIe and a synchronisation per call)
+    w = bh.make_tensor(packed, N, K, scale)
+    nw = bh.make_tensor(data=g)
+    out = np.empty(N, np.float32)
+    xn = np.empty(K, np.float32)
+    xq = np.zeros(K + 32, np.int8)
+    for _ in range(5):
+        L.hip_bitlinear_forward(bh.ptr(x), K, C.byref(w), C.byref(nw), bh.ptr(out), bh.ptr(xn),
+                                bh.ptr(xq))
+    t = []
+    for _ in range(50):
+        t0 = time.perf_counter()
+        L.hip_bitlinear_forward(bh.ptr(x), K, C.byref(w), C.byref(nw), bh.ptr(out), bh.ptr(xn),
+                                bh.ptr(xq))
+        t.append(time.perf_counter() - t0)
+    drop_us = float(np.median(t)) * 1e6
+    wbytes = N * K // 4
+    res = dict(gpu_device_us=round(dev_us, 2), gpu_device_GBps=round(wbytes / dev_us / 1e3, 1),
+               gpu_dropin_us=round(drop_us, 2), packed_bytes=wbytes,
+               note="device call = quantize + GEMV kernels on resident buffers (weights stay "
+                    "in cache between calls); drop-in = hip_bitlinear_forward on host buffers")
+    res.update(cpu_gemv1())
+    return res
+
+
+def cpu_gemv_child(threads, kind, reps=200):
+    """Times the reference's own bitlinear_forward (kind 1: what dispatch_init
+    picks here, AVX2; kind 0: scalar) on the K=1024 -> N=4384 inputs; median
+    of `reps` calls after warm-up.  Runs in a process without the GPU."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import native
+    R = native.ref()
+    name = R.bmref_init(threads, kind).decode()
+    R.bmref_set_poll(100)
+    packed, x, g, K, N, scale = gemv1_inputs()
+    out = np.empty(N, np.float32)
+    xn = np.empty(K, np.float32)
+    xq = np.zeros(K + 32, np.int8)
+    args = (native.ptr(x), K, native.ptr(packed), N, K, C.c_float(scale), native.ptr(g),
+            native.ptr(out), native.ptr(xn), native.ptr(xq))
+    for _ in range(20):
+        R.bmref_bitlinear_forward(*args)
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        R.bmref_bitlinear_forward(*args)
+        t.append(time.perf_counter() - t0)
+    R.bmref_shutdown()
+    print(json.dumps(dict(us=round(float(np.median(t)) * 1e6, 2), kernels=name,
+                          threads=threads)), flush=True)
+
+
+def cpu_gemv1():
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import native
+    import subprocess
+    if not native.ref_available():
+        return {}
+    out = {}
+    for key, threads, kind in (("cpu_avx2", cpu_threads(), 1), ("cpu_scalar", 1, 0)):
+        cmd = [sys.executable, os.path.abspath(__file__), "--cpu-gemv", str(threads), str(kind)]
+        try:
+            r = subprocess.run(cmd, stdout=subprocess.PIPE, timeout=120, text=True)
+        except subprocess.TimeoutExpired:
+            continue
+        lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+        if r.returncode == 0 and lines:
+            d = json.loads(lines[-1])
+            out[key + "_us"] = d["us"]
+            out[key + "_threads"] = d["threads"]
+            out[key + "_kernels"] = d["kernels"]
+    return out
+
+
+def leg_stress(L, reps=10):
+    K = N = 8192
+    w = bh.synth_ternary(5, 1, N, K, bh.SYNTH_P0_60)
+    dW = bh.DeviceBuffer.from_array(w)
+    del w
+    out = {}
+    ev = Events(L)
+    for M in (1, 16, 4096):
+        xq = bh.synth_int8(5, 2, (M, K))
+        dx = bh.DeviceBuffer.from_array(xq)
+        da = bh.DeviceBuffer(L.bm_hip_i8_act_bytes(M, K))
+        do = bh.DeviceBuffer(4 * M * N)
+        call = lambda: bh.check(L.bm_hip_ternary_gemm_i32_dev(dx.ptr, M, K, dW.ptr, N, K, 0,
+                                                              do.ptr, da.ptr, None), "stress")
+        for _ in range(2):
+            call()
+        ev.start()
+        for _ in range(reps):
+            call()
+        us = ev.stop_ms() * 1e3 / reps
+        r = dict(us=round(us, 2), tops=round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1))
+        if M < 4096:
+            r["weight_GBps_warm"] = round(N * K / 4 / (us * 1e-6) / 1e9, 1)
+        out["M%d" % M] = r
+        for b in (dx, da, do):
+            b.free()
+    dW.free()
+    out["note"] = ("int8 prep + product per call, canonical=0 (code 11 handled in-kernel); the "
+                   "16.8 MB weight tensor stays cache-resident across calls")
+    return out
 
 
 def leg_roofline(L, reps=5):
@@ -273,11 +433,14 @@ def main():
     if len(sys.argv) == 5 and sys.argv[1] == "--cpu-child":
         cpu_child(int(sys.argv[2]), int(sys.argv[3]), float(sys.argv[4]))
         return
+    if len(sys.argv) == 4 and sys.argv[1] == "--cpu-gemv":
+        cpu_gemv_child(int(sys.argv[2]), int(sys.argv[3]))
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--legs", default="decode,roofline,prefill,cpu")
+    ap.add_argument("--legs", default="decode,roofline,prefill,d255m,gemv1,stress,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (the BitLinear hot path at bs=1 "
@@ -299,6 +462,15 @@ def main():
     pre = leg_prefill(L) if "prefill" in legs else None
     if pre:
         log("prefill: %s" % json.dumps(pre))
+    d255 = leg_d255m(L) if "d255m" in legs else None
+    if d255:
+        log("255M-shape decode: %s" % json.dumps(d255))
+    g1 = leg_gemv1(L) if "gemv1" in legs else None
+    if g1:
+        log("K=1024 N=4384 BitLinear: %s" % json.dumps(g1))
+    strs = leg_stress(L) if "stress" in legs else None
+    if strs:
+        log("stress K=N=8192: %s" % json.dumps(strs))
     cpy = leg_copy(L) if "copy" in legs else None
     if cpy:
         log("copy: %s" % json.dumps(cpy))
@@ -326,6 +498,9 @@ def main():
         line.update(value=None, ms_per_step=None)
     line["roofline"] = roof
     line["prefill_gemm"] = pre
+    line["decode_255m"] = d255
+    line["bitlinear_k1024_n4384"] = g1
+    line["stress_k8192_n8192"] = strs
     line["cpu_baseline"] = cpu
     if cpy:
         line["copy_calibration"] = cpy
