@@ -396,25 +396,6 @@ __device__ __forceinline__ int dot64(uint4 w, const uint32_t (&xa)[16]) {
 // reduce a lane partial over its 16-lane slice group, subtract the slice's
 // sum of x, fold the slices of the T-lane row team in order into fp32
 // (src/kernel.c:255-256, 407-425)
-template <int T>
-__device__ __forceinline__ float row_finish(int part, int xs_slice, int p_index, int n_slices,
-                                            float inv, float o, int unit_base) {
-  part = row_sum_i32(part);
-  const float f = __fmul_rn((float)(part - xs_slice), inv);
-  if constexpr (T == 16) {
-    if (p_index < n_slices) o = __fadd_rn(o, f);
-  } else {
-    // the team's rows (16-lane slices) in order: rows unit_base/16 ..
-    const float r[4] = {lane_f32(f, 0), lane_f32(f, 16), lane_f32(f, 32), lane_f32(f, 48)};
-#pragma unroll
-    for (int q = 0; q < T / 16; ++q) {
-      const float fq = T == 64 ? r[q] : (unit_base == 0 ? r[q] : r[2 + q]);
-      if (p_index * (T / 16) + q < n_slices) o = __fadd_rn(o, fq);
-    }
-  }
-  return o;
-}
-
 template <int P, int T>
 __device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32_t (&xa)[P][16],
                                               int (&xsl)[P]) {

@@ -90,6 +90,43 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
+// A T-lane row team (T = 16, 32, 64; 16 lanes = one 1024-column slice)
+// holding one weight row: reduce each lane's partial x.code over its 16-lane
+// slice, subtract the slice's sum of x, and fold the team's slices into the
+// fp32 output in slice order (src/kernel.c:255-256, 407-425).
+template <int T>
+__device__ __forceinline__ float row_finish(int part, int xs_slice, int p_index, int n_slices,
+                                            float inv, float o, int unit_base) {
+  part = row_sum_i32(part);
+  const float f = __fmul_rn((float)(part - xs_slice), inv);
+  if constexpr (T == 16) {
+    if (p_index < n_slices) o = __fadd_rn(o, f);
+  } else {
+    // the team's rows (16-lane slices) in order: rows unit_base/16 ..
+    const float r[4] = {lane_f32(f, 0), lane_f32(f, 16), lane_f32(f, 32), lane_f32(f, 48)};
+#pragma unroll
+    for (int q = 0; q < T / 16; ++q) {
+      const float fq = T == 64 ? r[q] : (unit_base == 0 ? r[q] : r[2 + q]);
+      if (p_index * (T / 16) + q < n_slices) o = __fadd_rn(o, fq);
+    }
+  }
+  return o;
+}
+
+// the same team's exact int32 total (x.w over the team's columns)
+template <int T>
+__device__ __forceinline__ int row_total_i32(int part, int xs_slice, int unit_base) {
+  const int t = row_sum_i32(part) - xs_slice;
+  if constexpr (T == 16) {
+    return t;
+  } else {
+    const int r[4] = {__builtin_amdgcn_readlane(t, 0), __builtin_amdgcn_readlane(t, 16),
+                      __builtin_amdgcn_readlane(t, 32), __builtin_amdgcn_readlane(t, 48)};
+    if constexpr (T == 64) return (r[0] + r[1]) + (r[2] + r[3]);
+    return unit_base == 0 ? r[0] + r[1] : r[2] + r[3];
+  }
+}
+
 __device__ __forceinline__ float inv_scale_of(float scale_x, float w_scale) {
   return cr_divf(1.0f, __fmul_rn(scale_x, w_scale));  // src/kernel.c:391
 }

@@ -244,24 +244,11 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, s
         ah = __builtin_amdgcn_sdot8((int)lo, (int)xa[p][4 * d + 2], ah, false);
         ah = __builtin_amdgcn_sdot8((int)hi, (int)xa[p][4 * d + 3], ah, false);
       }
-      int part = ah * 16 + (int)al;
-      part += __shfl_xor(part, 8, 64);
-      part += __shfl_xor(part, 4, 64);
-      part += __shfl_xor(part, 2, 64);
-      part += __shfl_xor(part, 1, 64);
-      const int t = part - xs[p];  // exact slice total of x.w
-      if (I32) {
-#pragma unroll
-        for (int q = 0; q < T / 16; ++q) tot[i] += __shfl(t, unit_base + 16 * q, 64);
-      } else {
-        const float f = __fmul_rn((float)t, inv);
-#pragma unroll
-        for (int q = 0; q < T / 16; ++q) {
-          const float fq = __shfl(f, unit_base + 16 * q, 64);
-          // slices past K contribute nothing (they do not exist there)
-          if (p * (T / 16) + q < slices_of(K)) o[i] = __fadd_rn(o[i], fq);
-        }
-      }
+      const int part = ah * 16 + (int)al;
+      if (I32)
+        tot[i] += row_total_i32<T>(part, xs[p], unit_base);
+      else
+        o[i] = row_finish<T>(part, xs[p], p, slices_of(K), inv, o[i], unit_base);
     }
   }
   if (u == 0) {
@@ -275,6 +262,135 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ act, s
           out[(size_t)m * N + row] = MODE == 1 ? __fadd_rn(out[(size_t)m * N + row], o[i]) : o[i];
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Few-token GEMV (2 <= M < 32): the k_gemv row layout, but each wave loads
+// its weight rows once and applies them to every token in turn.  A token's
+// activations (split nibbles + slice sums) are staged in LDS for the whole
+// block, double-buffered through registers one token ahead.  K <= 8192.
+// ---------------------------------------------------------------------------
+constexpr int kMtMaxK = 8192, kMtMaxM = 32;
+
+template <int T, int P, int GW, bool CANON, int MODE>
+__global__ __launch_bounds__(256) void k_gemv_mt(const uint8_t* __restrict__ act,
+                                                 size_t act_stride,
+                                                 const float* __restrict__ scale_x, int M,
+                                                 const uint8_t* __restrict__ W, int N, int K,
+                                                 float w_scale, float* __restrict__ out,
+                                                 int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
+  constexpr int RPW = 64 / T;
+  constexpr int SU = kMtMaxK / 16 / 256;  // staged uint4 per thread per token
+  __shared__ uint4 s_nib[2][kMtMaxK / 16];
+  __shared__ int s_sl[2][kMtMaxK / 1024];
+  __shared__ float s_inv[kMtMaxM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int u = lane % T, sub = lane / T, unit_base = sub * T;
+  const int n_rg = (N + RPW - 1) / RPW;
+  const int rg0 = (blockIdx.x * 4 + wave) * GW;
+  const int chunks = K >> 6, n_groups16 = K >> 4, n_sl = slices_of(K);
+  const size_t wstride = (size_t)(K >> 2);
+  const size_t nib_off = act_nib_off(K);
+
+  if (tid < M) s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[tid], w_scale);
+
+  // this wave's weights, once
+  uint4 wv[GW][P];
+#pragma unroll
+  for (int i = 0; i < GW; ++i) {
+    const int r = min((rg0 + i) * RPW + sub, N - 1);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = min(p * T + u, chunks - 1);
+      wv[i][p] = load_stream16(W + (size_t)r * wstride + 16 * (size_t)j);
+    }
+  }
+
+  // token m's activations: global -> registers -> LDS buffer m & 1
+  uint4 st_nib[SU];
+  int st_sl = 0;
+  auto fetch = [&](int m) __attribute__((always_inline)) {
+    const uint8_t* __restrict__ arow = act + (size_t)min(m, M - 1) * act_stride;
+#pragma unroll
+    for (int k = 0; k < SU; ++k) {
+      const int g = tid + 256 * k;
+      st_nib[k] = g < n_groups16 ? ((const uint4*)(arow + nib_off))[g] : make_uint4(0, 0, 0, 0);
+    }
+    st_sl = tid < n_sl ? ((const int*)arow)[tid] : 0;
+  };
+  auto put = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < SU; ++k) {
+      const int g = tid + 256 * k;
+      if (g < n_groups16) s_nib[buf][g] = st_nib[k];
+    }
+    if (tid < n_sl) s_sl[buf][tid] = st_sl;
+  };
+
+  fetch(0);
+  put(0);
+  fetch(1);
+  __syncthreads();
+  for (int m = 0; m < M; ++m) {
+    const int buf = m & 1;
+    uint32_t xa[P][16];
+    int xs[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = p * T + u;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint4 v = j < chunks ? s_nib[buf][4 * j + g] : make_uint4(0, 0, 0, 0);
+        xa[p][4 * g + 0] = v.x;
+        xa[p][4 * g + 1] = v.y;
+        xa[p][4 * g + 2] = v.z;
+        xa[p][4 * g + 3] = v.w;
+      }
+      const int slice = (p * T + u) / 16;
+      xs[p] = slice < n_sl ? s_sl[buf][slice] : 0;
+    }
+    const float inv = s_inv[m];
+    if (rg0 < n_rg) {
+#pragma unroll
+      for (int i = 0; i < GW; ++i) {
+        float o = 0.0f;
+        int tot = 0;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const uint32_t w4[4] = {wv[i][p].x, wv[i][p].y, wv[i][p].z, wv[i][p].w};
+          uint32_t al = 0;
+          int ah = 0;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t pw = CANON ? w4[d] : canon_codes(w4[d]);
+            const uint32_t lo = pw & 0x33333333u;
+            const uint32_t hi = (pw >> 2) & 0x33333333u;
+            al = __builtin_amdgcn_udot8(lo, xa[p][4 * d + 0], al, false);
+            al = __builtin_amdgcn_udot8(hi, xa[p][4 * d + 1], al, false);
+            ah = __builtin_amdgcn_sdot8((int)lo, (int)xa[p][4 * d + 2], ah, false);
+            ah = __builtin_amdgcn_sdot8((int)hi, (int)xa[p][4 * d + 3], ah, false);
+          }
+          const int part = ah * 16 + (int)al;
+          if (I32)
+            tot += row_total_i32<T>(part, xs[p], unit_base);
+          else
+            o = row_finish<T>(part, xs[p], p, n_sl, inv, o, unit_base);
+        }
+        const int row = (rg0 + i) * RPW + sub;
+        if (u == 0 && rg0 + i < n_rg && row < N) {
+          const size_t at = (size_t)m * N + row;
+          if (I32)
+            out_i32[at] = tot;
+          else
+            out[at] = MODE == 1 ? __fadd_rn(out[at], o) : o;
+        }
+      }
+    }
+    put(buf ^ 1);  // token m+1 into the buffer token m-1 used
+    fetch(m + 2);
+    __syncthreads();
   }
 }
 
@@ -632,9 +748,28 @@ static hipError_t gemv_t(const uint8_t* act, const float* scale_x, int M, const 
   return go(std::integral_constant<int, 1>());
 }
 
+template <int T, int P, bool CANON, int MODE>
+static hipError_t gemv_mt_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
+                            int N, int K, float w_scale, void* out, hipStream_t s) {
+  constexpr int RPW = 64 / T;
+  constexpr int GW = P == 1 ? 8 : 4;
+  const long long n_rg = (N + RPW - 1) / RPW;
+  const long long waves = (n_rg + GW - 1) / GW;
+  hipLaunchKernelGGL((k_gemv_mt<T, P, GW, CANON, MODE>), dim3((unsigned)((waves + 3) / 4)),
+                     dim3(256), 0, s, act, act_row_bytes(K), scale_x, M, W, N, K, w_scale,
+                     (float*)out, (int32_t*)out);
+  return hipGetLastError();
+}
+
 template <bool CANON, int MODE>
 static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
                                 int N, int K, float w_scale, void* out, hipStream_t s) {
+  if (M >= 2 && M <= kMtMaxM && K <= kMtMaxK) {
+    if (K <= 1024) return gemv_mt_t<16, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+    if (K <= 2048) return gemv_mt_t<32, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+    if (K <= 4096) return gemv_mt_t<64, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+    return gemv_mt_t<64, 2, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  }
   if (K <= 1024) return gemv_t<16, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
   if (K <= 2048) return gemv_t<32, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
   if (K <= 4096) return gemv_t<64, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);

@@ -129,7 +129,8 @@ def test_gemv_i32_exact(hip, K, N, canonical):
 @pytest.mark.parametrize("M,K,N", [(32, 1024, 128), (100, 2048, 200), (256, 1024, 333),
                                    (64, 4096, 64), (40, 8192, 129), (16, 8192, 512),
                                    (3, 1024, 50), (300, 1152, 260), (700, 2048, 1100),
-                                   (1100, 1024, 700), (48, 16384, 96)])
+                                   (1100, 1024, 700), (48, 16384, 96), (2, 2048, 77),
+                                   (31, 4096, 300), (5, 8192, 33)])
 def test_gemm_i32_exact(hip, M, K, N):
     note("gemm i32 M=%d K=%d N=%d" % (M, K, N))
     r = rnd(M * 3 + K + N)
