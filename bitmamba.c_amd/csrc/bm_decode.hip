@@ -40,38 +40,6 @@ __device__ __forceinline__ float softplus_r(float x) {
 // Sum of squares: four sequential chains
 // ---------------------------------------------------------------------------
 
-// chains held in registers (K/64 = E in {16, 32, 64}): lanes 16j..16j+15 of
-// wave 0 own chain j in segments of E consecutive elements; each lane adds
-// its segment to the running sum, which then moves one lane up the 16-lane
-// row (DPP row_shr:1).  After 16 rounds lane 16j+15 holds chain j's sum.
-__host__ __device__ inline bool chain_in_regs(int K) { return K == 1024 || K == 2048 || K == 4096; }
-__host__ __device__ inline int sq_stride_of(int K) { return K / 4 + 68; }
-
-template <int E>
-__device__ __forceinline__ float chain_regs(const float* __restrict__ sq, int stride, int lane) {
-  const int j = lane >> 4, seg = lane & 15;
-  const float* __restrict__ src = sq + j * stride + seg * (E + 4);
-  float v[E];
-#pragma unroll
-  for (int u = 0; u < E / 4; ++u) {
-    const float4 t = *(const float4*)(src + 4 * u);
-    v[4 * u] = t.x;
-    v[4 * u + 1] = t.y;
-    v[4 * u + 2] = t.z;
-    v[4 * u + 3] = t.w;
-  }
-  float s = 0.0f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-#pragma unroll
-    for (int k = 0; k < E; ++k) s = __fadd_rn(s, v[k]);
-    if (r < 15)
-      s = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(s), __float_as_int(s), 0x111,
-                                                     0xf, 0xf, false));
-  }
-  return s;
-}
-
 // other K: one lane per chain over LDS, two 32-value buffers alternating
 __device__ __forceinline__ void add32(float& s, const float4 (&b)[8]) {
 #pragma unroll

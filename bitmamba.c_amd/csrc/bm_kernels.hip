@@ -134,6 +134,131 @@ __global__ __launch_bounds__(QT) void k_quantize(const float* __restrict__ x, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Quantizer for n = 1024 * G (G in {1, 2, 4}): one wave per token, four
+// tokens per block (two at G = 4), no block barriers.  Lane l keeps the 16-column groups
+// l + 64i in registers; the squares pass through the wave's own LDS region
+// once to reach the four-chain layout; everything else is register work.
+// Same numerics as k_quantize.
+// ---------------------------------------------------------------------------
+// tokens (waves) per block: four, two at n = 4096 (LDS <= 64 KiB per block)
+__host__ __device__ inline int quantize_wave_tpb(int n) { return n >= 4096 ? 2 : 4; }
+__host__ __device__ inline size_t quantize_wave_lds(int n) {
+  return (size_t)quantize_wave_tpb(n) * 4 * (size_t)sq_stride_of(n) * sizeof(float);
+}
+
+template <int G>
+__global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const float* __restrict__ x, int M,
+                                                       int x_stride,
+                                                       const float* __restrict__ gamma,
+                                                       float* __restrict__ x_norm,
+                                                       int8_t* __restrict__ xq, int quant_stride,
+                                                       float* __restrict__ scale_out,
+                                                       uint8_t* __restrict__ act,
+                                                       size_t act_stride) {
+  constexpr int K = 1024 * G, E = K / 64;
+  extern __shared__ __attribute__((aligned(16))) float lds_sq[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = blockIdx.x * (G == 4 ? 2 : 4) + wave;
+  if (m >= M) return;  // whole waves only; nothing below waits for other waves
+  const int stride = sq_stride_of(K);
+  float* __restrict__ sq = lds_sq + (size_t)wave * 4 * stride;
+  const float* __restrict__ xr = x + (size_t)m * x_stride;
+
+  float4 xv[G][4], gv[G][4];
+#pragma unroll
+  for (int i = 0; i < G; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c4 = 4 * (lane + 64 * i) + k;
+      xv[i][k] = ((const float4*)xr)[c4];
+      gv[i][k] = ((const float4*)gamma)[c4];
+    }
+  // column 16g + 4k + j is element 4g + k of chain j (segments of E padded
+  // by 4 floats)
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int e = 4 * (lane + 64 * i);
+    const int pe = e + 4 * (e / E);
+    const float4* v = xv[i];
+    *(float4*)&sq[pe] = make_float4(__fmul_rn(v[0].x, v[0].x), __fmul_rn(v[1].x, v[1].x),
+                                    __fmul_rn(v[2].x, v[2].x), __fmul_rn(v[3].x, v[3].x));
+    *(float4*)&sq[stride + pe] = make_float4(__fmul_rn(v[0].y, v[0].y), __fmul_rn(v[1].y, v[1].y),
+                                             __fmul_rn(v[2].y, v[2].y), __fmul_rn(v[3].y, v[3].y));
+    *(float4*)&sq[2 * stride + pe] =
+        make_float4(__fmul_rn(v[0].z, v[0].z), __fmul_rn(v[1].z, v[1].z),
+                    __fmul_rn(v[2].z, v[2].z), __fmul_rn(v[3].z, v[3].z));
+    *(float4*)&sq[3 * stride + pe] =
+        make_float4(__fmul_rn(v[0].w, v[0].w), __fmul_rn(v[1].w, v[1].w),
+                    __fmul_rn(v[2].w, v[2].w), __fmul_rn(v[3].w, v[3].w));
+  }
+  // one wave's LDS operations complete in order; the fences keep the
+  // compiler from moving the reads above the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float cs = chain_regs<E>(sq, stride, lane);
+  const float s0 = lane_f32(cs, 15), s1 = lane_f32(cs, 31);
+  const float s2 = lane_f32(cs, 47), s3 = lane_f32(cs, 63);
+  const float sum = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
+  // sum / K with K a power of two: an exact scaling, rounded like the division
+  const float rms = cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(sum, 1.0f / K), 1e-6f)));
+
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < G; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 v = xv[i][k];
+      const float4 g4 = gv[i][k];
+      xv[i][k] = make_float4(__fmul_rn(__fmul_rn(v.x, rms), g4.x), __fmul_rn(__fmul_rn(v.y, rms), g4.y),
+                             __fmul_rn(__fmul_rn(v.z, rms), g4.z), __fmul_rn(__fmul_rn(v.w, rms), g4.w));
+      if (x_norm) ((float4*)(x_norm + (size_t)m * K))[4 * (lane + 64 * i) + k] = xv[i][k];
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[i][k].x), fabsf(xv[i][k].y)),
+                           fmaxf(fabsf(xv[i][k].z), fabsf(xv[i][k].w))));
+    }
+  mx = wave_max_f32(mx);
+  const float scale_x = cr_divf(127.0f, __fadd_rn(mx, 1e-5f));
+  if (lane == 0 && scale_out) scale_out[m] = scale_x;
+
+  uint8_t* __restrict__ arow = act ? act + (size_t)m * act_stride : nullptr;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = lane + 64 * i;
+    int q[16];
+    int qsum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float vv[4] = {xv[i][k].x, xv[i][k].y, xv[i][k].z, xv[i][k].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float t = __fmul_rn(vv[j], scale_x);
+        int iv = (int)__fadd_rn(t, t >= 0.0f ? 0.5f : -0.5f);
+        iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+        q[4 * k + j] = iv;
+        qsum += iv;
+      }
+    }
+    if (xq) {
+      int8_t* dst = xq + (size_t)m * quant_stride + 16 * g;
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        w[k] = (uint32_t)(q[4 * k] & 255) | ((uint32_t)(q[4 * k + 1] & 255) << 8) |
+               ((uint32_t)(q[4 * k + 2] & 255) << 16) | ((uint32_t)(q[4 * k + 3] & 255) << 24);
+      if (((uintptr_t)dst & 15) == 0) {
+        *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dst[j] = (int8_t)q[j];
+      }
+    }
+    if (arow) write_act_group(arow, K, g, q);
+    const int ssum = wave_sum_i32(qsum);  // groups 64i .. 64i+63 = slice i
+    if (arow && lane == 0) ((int*)arow)[i] = ssum;
+  }
+}
+
 // int8 activations given directly (stress shape): workspace only
 __global__ __launch_bounds__(QT) void k_prep_i8(const int8_t* __restrict__ xq, int ldx, int K,
                                                 uint8_t* __restrict__ act, size_t act_stride) {
@@ -708,6 +833,24 @@ hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const flo
                            float* x_norm, int8_t* xq, int quant_stride, float* scale_x,
                            uint8_t* act, hipStream_t s) {
   if (M <= 0) return hipSuccess;
+  // one wave per token when the rows allow 16-byte loads of whole groups
+  const bool aligned = ((uintptr_t)x % 16 == 0) && (x_stride % 4 == 0) &&
+                       ((uintptr_t)gamma % 16 == 0) && (!x_norm || (uintptr_t)x_norm % 16 == 0);
+  if (aligned && (n == 1024 || n == 2048 || n == 4096)) {
+    const int tpb = quantize_wave_tpb(n);
+    const dim3 grid((M + tpb - 1) / tpb), block(64 * tpb);
+    const size_t lds = quantize_wave_lds(n);
+    if (n == 1024)
+      hipLaunchKernelGGL(k_quantize_wave<1>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
+                         xq, quant_stride, scale_x, act, act_row_bytes(n));
+    else if (n == 2048)
+      hipLaunchKernelGGL(k_quantize_wave<2>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
+                         xq, quant_stride, scale_x, act, act_row_bytes(n));
+    else
+      hipLaunchKernelGGL(k_quantize_wave<4>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
+                         xq, quant_stride, scale_x, act, act_row_bytes(n));
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_quantize, dim3(M), dim3(QT), 0, s, x, n, x_stride, gamma, x_norm, xq,
                      quant_stride, scale_x, (float*)nullptr, act, act_row_bytes(n));
   return hipGetLastError();
