@@ -584,9 +584,10 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 //   block 256 threads = 2x2 waves, tile 128(M) x 128(N), each wave 64 x 64
 //   (2 x 2 MFMA tiles); K in stages of 128.
 //   Each stage (A: 128 rows x 128 permuted int8 activations; B: 128 weight
-//   rows x 32 packed bytes) is loaded into registers two stages ahead and
-//   written to one of two LDS buffers one stage ahead, so a load has two
-//   stages of MFMA work to arrive in; one barrier per stage.  LDS serves a
+//   rows x 32 packed bytes) is loaded into registers three stages ahead and
+//   written to one of three LDS buffers at the start of the stage before
+//   its use, so a load has two stages of MFMA work to arrive in and the
+//   LDS writes overlap the MFMAs; one barrier per stage.  LDS serves a
 //   16-byte read for 16 lanes per cycle from 64 banks: A's 16-byte chunks
 //   are XOR-swizzled by row/2 and B's two 16-byte halves by row/8, so the
 //   operand reads of 16 consecutive rows hit 16 different bank groups.
@@ -637,8 +638,8 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
   constexpr int GBN = 64 * WN, NT = 128 * WN;  // tile columns, threads
   constexpr int NA = 8 / WN;                  // A chunks per thread per stage
   constexpr int BB = GBK / 4;                 // packed bytes per weight row per stage
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][GBM * GBK];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][GBN * BB];
+  __shared__ __attribute__((aligned(16))) uint8_t sA[3][GBM * GBK];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[3][GBN * BB];
   __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][GBM];
   __shared__ __attribute__((aligned(16))) float s_inv[GBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -700,10 +701,15 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
         o[a][b][v] = 0.0f;
       }
 
-  // one stage: X holds stage st+1 (in flight), Y is free and receives st+2
-  auto body = [&](int st, GemmStage<WN>& X, GemmStage<WN>& Y) __attribute__((always_inline)) {
-    const uint8_t* __restrict__ cA = sA[st & 1];
-    const uint8_t* __restrict__ cB = sB[st & 1];
+  // one stage: X holds stage st+1 (loaded two stages ago) and goes to LDS
+  // first, so that the barrier closing the stage finds the writes long done;
+  // Y holds stage st+2 (in flight); Z is free and receives stage st+3
+  auto body = [&](int st, GemmStage<WN>& X, GemmStage<WN>& Y, GemmStage<WN>& Z)
+                  __attribute__((always_inline)) {
+    (void)Y;
+    store_stage((st + 1) % 3, X);  // the buffer stage st-2 used
+    const uint8_t* __restrict__ cA = sA[st % 3];
+    const uint8_t* __restrict__ cB = sB[st % 3];
     v4i aop[2][4];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -718,7 +724,7 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
       const int col = wn * 64 + nt * 32 + j32;
       bw[nt] = *(const uint4*)(cB + col * BB + 16 * (h ^ ((col >> 3) & 1)));
     }
-    load_stage(st + 2, Y);
+    load_stage(st + 3, Z);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       v4i bop[2];
@@ -764,23 +770,25 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
         }
       }
     }
-    store_stage((st + 1) & 1, X);  // the buffer stage st-1 used
     __syncthreads();
   };
 
-  GemmStage<WN> R0, R1;
+  GemmStage<WN> R0, R1, R2;
   load_stage(0, R0);
   load_stage(1, R1);
+  load_stage(2, R2);
   store_stage(0, R0);
   __syncthreads();
-  // two stages per turn so that each register set keeps its registers (no
+  // three stages per turn so that each register set keeps its registers (no
   // mid-turn exit: a merge there makes the loop head wait for every load)
   int st = 0;
-  for (; st + 2 <= n_stages; st += 2) {
-    body(st, R1, R0);
-    body(st + 1, R0, R1);
+  for (; st + 3 <= n_stages; st += 3) {
+    body(st, R1, R2, R0);
+    body(st + 1, R2, R0, R1);
+    body(st + 2, R0, R1, R2);
   }
-  if (st < n_stages) body(st, R1, R0);
+  if (st < n_stages) body(st, R1, R2, R0);
+  if (st + 1 < n_stages) body(st + 1, R2, R0, R1);
 
   if (I32) {
     // exact totals: x.code over all of K minus the sum of x over all slices
