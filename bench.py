@@ -23,6 +23,10 @@ Prints ONE JSON line.  Legs (all by default):
   d255m     255M-shape greedy decode, 128 steps (tok/s, stream identity)
   stress    int8-input ternary products at K = N = 8192, p(0) = 0.6, exact
             int32 outputs: M = 1, 16 (weight GB/s, warm) and 4096 (TOP/s)
+  mfma      the int8 MFMA ceiling: 2 waves per SIMD of back-to-back
+            v_mfma_i32_32x32x32_i8, fixed operands and then hashed int8
+            activations against codes 0..2 (the GEMM's data; the sustained
+            rate depends on the data through the clock under load)
   copy      (on request only) a plain 512 MiB device copy: the calibration
             run for the HBM traffic counters
 The roofline's `traffic` (HBM bytes per launch of the GEMV) is read from
@@ -321,6 +325,21 @@ def leg_copy(L, reps=5):
                 GBps_read_plus_write=round(2 * n / (ms * 1e-3) / 1e9, 1))
 
 
+def leg_mfma(L, iters=2000):
+    sink = bh.DeviceBuffer(4)
+    ev = Events(L)
+    blocks = 512  # 256-thread blocks: two waves on every SIMD of the 256 CUs
+    out = {}
+    for name, tern in (("fixed_operands_tops", 0), ("ternary_operands_tops", 1)):
+        bh.check(L.bm_hip_mfma_peak_dev(blocks, 50, tern, sink.ptr, None), "mfma")
+        ev.start()
+        bh.check(L.bm_hip_mfma_peak_dev(blocks, iters, tern, sink.ptr, None), "mfma")
+        ms = ev.stop_ms()
+        out[name] = round(blocks * 4 * iters * 16 * 65536.0 / (ms * 1e-3) / 1e12, 1)
+    sink.free()
+    return out
+
+
 def leg_prefill(L, reps=10):
     out = {}
     ev = Events(L)
@@ -440,7 +459,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--legs", default="decode,roofline,prefill,d255m,gemv1,stress,cpu")
+    ap.add_argument("--legs", default="decode,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (the BitLinear hot path at bs=1 "
@@ -459,7 +478,13 @@ def main():
     if roof:
         log("roofline: %.1f GB/s (%.1f%% of HBM peak), %.1f us per launch"
             % (roof["achieved"], 100 * roof["frac"], roof["launch_us"]))
+    mf = leg_mfma(L) if "mfma" in legs else None
+    if mf:
+        log("mfma ceiling: %s" % json.dumps(mf))
     pre = leg_prefill(L) if "prefill" in legs else None
+    if pre and mf:
+        for v in pre.values():
+            v["frac_of_ternary_ceiling"] = round(v["tops"] / mf["ternary_operands_tops"], 4)
     if pre:
         log("prefill: %s" % json.dumps(pre))
     d255 = leg_d255m(L) if "d255m" in legs else None
@@ -497,6 +522,7 @@ def main():
     else:
         line.update(value=None, ms_per_step=None)
     line["roofline"] = roof
+    line["mfma_ceiling"] = mf
     line["prefill_gemm"] = pre
     line["decode_255m"] = d255
     line["bitlinear_k1024_n4384"] = g1

@@ -64,6 +64,7 @@ SIGNATURES = {
     "bm_hip_event_record": (_i, [_vp, _vp]),
     "bm_hip_event_elapsed_ms": (_f, [_vp, _vp]),
     "bm_hip_copy_dev": (_i, [_vp, _vp, _sz, _vp]),
+    "bm_hip_mfma_peak_dev": (_i, [_i, _i, _i, _vp, _vp]),
     "bm_hip_act_bytes": (_sz, [_i, _i]),
     "bm_hip_quantize_dev": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "bm_hip_bitlinear_act_dev": (_i, [_vp, _vp, _i, _vp, _i, _i, _f, _i, _vp, _vp]),

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "bm_common.h"
+#include "bm_dev.h"
 #include "bm_hip.h"
 #include "bm_bit2.h"
 
@@ -561,6 +562,70 @@ __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst,
     dst[i] = src[i];
 }
 }  // namespace bm
+
+namespace bm {
+// int8 MFMA ceiling: each wave runs `iters` rounds of 16 v_mfma_i32_32x32x32_i8
+// on four accumulators.  Operands are fixed small integers (ternary = 0) or,
+// like the prefill GEMM's, hashed int8 activations against codes 0..2
+// (ternary = 1): the sustained rate depends on the data (clock under load).
+__global__ __launch_bounds__(256) void k_mfma_peak(int iters, int ternary, int* __restrict__ sink) {
+  v16i acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0;
+  v4i opa[2][4], opb[2][4];
+  uint32_t z = (threadIdx.x + 1) * 2654435761u ^ (blockIdx.x + 1) * 40503u;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        z ^= z << 13;
+        z ^= z >> 17;
+        z ^= z << 5;
+        const uint32_t w = z;
+        z ^= z << 13;
+        z ^= z >> 17;
+        z ^= z << 5;
+        uint32_t c = z & 0x03030303u;
+        c -= (c >> 1) & (c & 0x01010101u);  // code 3 -> 2
+        opa[a][q][e] = ternary ? (int)w : (int)(threadIdx.x + e);
+        opb[a][q][e] = ternary ? (int)c : (int)(q + a);
+      }
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] =
+              __builtin_amdgcn_mfma_i32_32x32x32_i8(opa[mt][q], opb[nt][q], acc[mt][nt], 0, 0, 0);
+  }
+  int r = 0;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) r ^= acc[a][b][0] ^ acc[a][b][15];
+  if (r == 0x5eed5eed) sink[0] = r;  // keeps the MFMAs live
+}
+}  // namespace bm
+
+extern "C" int bm_hip_mfma_peak_dev(int blocks, int iters, int ternary, int* sink, void* stream) {
+  if (!bm_hip_init()) return -1;
+  if (blocks < 1 || iters < 1) {
+    bm_set_error("mfma_peak: blocks and iters must be positive");
+    return -2;
+  }
+  hipLaunchKernelGGL(bm::k_mfma_peak, dim3(blocks), dim3(256), 0, stream_or_default(stream), iters,
+                     ternary, sink);
+  BM_HIP_CHECK_RET(hipGetLastError(), -1);
+  return 0;
+}
 
 extern "C" int bm_hip_copy_dev(void* dst, const void* src, size_t bytes, void* stream) {
   if (!bm_hip_init()) return -1;

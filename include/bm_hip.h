@@ -158,6 +158,11 @@ void bm_hip_event_destroy(void *ev);
 int bm_hip_event_record(void *ev, void *stream);
 float bm_hip_event_elapsed_ms(void *start, void *stop);
 int bm_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
+/* int8 MFMA ceiling: `blocks` blocks of 256 threads, each wave `iters` x 16
+ * v_mfma_i32_32x32x32_i8 (65536 ops each); ternary != 0 uses hashed int8
+ * activations against codes 0..2 like the prefill GEMM.  `sink` (one int,
+ * device) is written only on an impossible value. */
+int bm_hip_mfma_peak_dev(int blocks, int iters, int ternary, int *sink, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Device-pointer kernels (asynchronous on `stream`)                    */
