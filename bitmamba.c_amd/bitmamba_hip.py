@@ -78,6 +78,8 @@ SIGNATURES = {
     "bm_hip_model_reset": (_i, [_vp]),
     "bm_hip_model_prefill": (_i, [_vp, _vp, _i]),
     "bm_hip_model_step": (_i, [_vp, _i, _vp, _i, _f]),
+    "bm_hip_model_set_sampler": (_i, [_vp, _f, _f, _f, _i]),
+    "bm_hip_model_seed": (_i, [_vp, _u64]),
     "bm_hip_model_logits": (_i, [_vp, _vp]),
     "bm_hip_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
     "bm_hip_model_generate": (_i, [_vp, _vp, _i, _i, _f, _i, _vp, C.POINTER(C.c_double)]),
@@ -253,6 +255,12 @@ class Model:
         if r < 0:
             raise RuntimeError("step: " + last_error())
         return r
+
+    def set_sampler(self, temp=0.0, min_p=0.0, top_p=1.0, top_k=0):
+        check(lib().bm_hip_model_set_sampler(self.h, temp, min_p, top_p, top_k), "set_sampler")
+
+    def seed(self, seed):
+        check(lib().bm_hip_model_seed(self.h, seed), "seed")
 
     def logits(self):
         out = np.empty(self.vocab, np.float32)

@@ -197,6 +197,10 @@ hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const floa
                           float* part_v, int* part_i, hipStream_t s);
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,
                        int* out_tokens, const float* embed, int dm, float* x, hipStream_t s);
+size_t sample_scratch_bytes(int V);
+hipError_t launch_sample(float* logits, int V, float temp, float min_p, float top_p, int top_k,
+                         uint64_t* rng_state, void* scratch, int* ctl, int* hist, int* out_tokens,
+                         hipStream_t s);
 
 }  // namespace bm
 
@@ -241,11 +245,17 @@ struct bm_hip_model {
   int8_t* pxq = nullptr;
   int* ptok = nullptr;
   int pcap = 0;
+  // sampler (src/model.c:132-361): temp < 0.05 is greedy
+  float temp = 0.0f, min_p = 0.0f, top_p = 1.0f;
+  int top_k = 0;
+  uint64_t* rng = nullptr;      // XorShift64* state (src/utils.c:117-134)
+  void* samp_scratch = nullptr;
   // captured decode step
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   float graph_penalty = 1.0f;
   bool graph_with_out = false;
+  float graph_samp[4] = {0.0f, 0.0f, 1.0f, 0.0f};
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   // BM_HIP_NO_GRAPH=1: enqueue each step's kernels directly instead of
   // replaying the captured graph (for tools that cannot trace graphs)
@@ -303,11 +313,23 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
     }
     MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s));
   }
-  const bool fused_pick = penalty == 1.0f;  // x / 1.0f == x * 1.0f == x
+  const bool sampled = !(m->temp < 0.05f);  // src/model.c:143-144
+  const bool fused_pick = penalty == 1.0f && !sampled;  // x / 1.0f == x * 1.0f == x
   MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab, m->lm_scale,
                             m->logits, fused_pick, m->part_v, m->part_i, s));
   int* out = write_out ? m->out_tokens : nullptr;
-  if (fused_pick) {
+  if (sampled) {
+    if (penalty != 1.0f) {
+      hipLaunchKernelGGL(bm::k_penalty, dim3(1), dim3(bm::kHistory), 0, s, m->logits, m->vocab,
+                         m->hist, m->ctl, penalty);
+      MCHECK(hipGetLastError());
+    }
+    MCHECK(bm::launch_sample(m->logits, m->vocab, m->temp, m->min_p, m->top_p, m->top_k, m->rng,
+                             m->samp_scratch, m->ctl, m->hist, out, s));
+    hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, 1), dim3(256), 0, s, m->embed, dm,
+                       m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
+    MCHECK(hipGetLastError());
+  } else if (fused_pick) {
     MCHECK(bm::launch_pick(m->part_v, m->part_i, m->lm_blocks, m->ctl, m->hist, out, m->embed, dm,
                            m->x, s));
   } else {
@@ -330,7 +352,10 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
     m->graph_with_out = write_out;
     return 0;
   }
-  if (m->exec && m->graph_penalty == penalty && m->graph_with_out == write_out) return 0;
+  const float samp[4] = {m->temp, m->min_p, m->top_p, (float)m->top_k};
+  if (m->exec && m->graph_penalty == penalty && m->graph_with_out == write_out &&
+      memcmp(samp, m->graph_samp, sizeof(samp)) == 0)
+    return 0;
   if (m->exec) {
     (void)hipGraphExecDestroy(m->exec);
     m->exec = nullptr;
@@ -352,6 +377,7 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
   MCHECK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
   m->graph_penalty = penalty;
   m->graph_with_out = write_out;
+  memcpy(m->graph_samp, samp, sizeof(samp));
   return 0;
 }
 
@@ -380,7 +406,7 @@ void model_release(bm_hip_model* m) {
   for (void* p : {(void*)m->arena, (void*)m->conv_state, (void*)m->ssm_state, (void*)m->ctl,
                   (void*)m->hist, (void*)m->out_tokens, (void*)m->x, (void*)m->proj,
                   (void*)m->y, (void*)m->feat, (void*)m->logits, (void*)m->scale,
-                  (void*)m->part_v, (void*)m->part_i,
+                  (void*)m->part_v, (void*)m->part_i, (void*)m->rng, m->samp_scratch,
                   (void*)m->act, (void*)m->xq, (void*)m->px, (void*)m->pproj, (void*)m->py,
                   (void*)m->pscale, (void*)m->pact, (void*)m->pxq, (void*)m->ptok})
     if (p) (void)hipFree(p);
@@ -523,6 +549,12 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
   MCHECK(hipMalloc(&m->part_v, (size_t)m->lm_blocks * 4));
   MCHECK(hipMalloc(&m->part_i, (size_t)m->lm_blocks * 4));
   MCHECK(hipMalloc(&m->scale, 64));
+  MCHECK(hipMalloc(&m->rng, sizeof(uint64_t)));
+  {
+    const uint64_t seed0 = 0x853c49e6748fea9bULL;  // src/utils.c:119
+    MCHECK(hipMemcpy(m->rng, &seed0, sizeof(seed0), hipMemcpyHostToDevice));
+  }
+  MCHECK(hipMalloc(&m->samp_scratch, bm::sample_scratch_bytes(m->vocab)));
   MCHECK(hipMalloc(&m->act, bm::act_row_bytes(di > dm ? di : dm)));
   MCHECK(hipMalloc(&m->xq, (size_t)(di > dm ? di : dm)));
   MCHECK(hipDeviceSynchronize());
@@ -662,6 +694,22 @@ extern "C" int bm_hip_model_step(bm_hip_model_t* m, int token, const int* histor
   MCHECK(hipMemcpyAsync(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost, m->stream));
   MCHECK(hipStreamSynchronize(m->stream));
   return ctl[bm::CTL_TOKEN];
+}
+
+extern "C" int bm_hip_model_set_sampler(bm_hip_model_t* m, float temp, float min_p, float top_p,
+                                        int top_k) {
+  m->temp = temp;
+  m->min_p = min_p;
+  m->top_p = top_p;
+  m->top_k = top_k;
+  return 0;
+}
+
+extern "C" int bm_hip_model_seed(bm_hip_model_t* m, uint64_t seed) {
+  const uint64_t s = seed ? seed : 0x853c49e6748fea9bULL;  // rng_seed (src/utils.c:121-124)
+  MCHECK(hipMemcpyAsync(m->rng, &s, sizeof(s), hipMemcpyHostToDevice, m->stream));
+  MCHECK(hipStreamSynchronize(m->stream));
+  return 0;
 }
 
 extern "C" int bm_hip_model_logits(const bm_hip_model_t* m, float* out) {

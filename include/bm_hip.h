@@ -237,8 +237,8 @@ int bm_hip_ternary_gemm_i32_dev(const int8_t *xq,
 /* ------------------------------------------------------------------ */
 /* Device-resident model: the reference's model API (src/bitmamba.h:    */
 /* 282-294, src/model.c:477-1314) with weights, activations and the    */
-/* recurrent state in HBM.  Greedy sampling only (temp < 0.05,         */
-/* src/model.c:143-154); repetition penalty supported.                 */
+/* recurrent state in HBM.  Greedy or sampled next tokens              */
+/* (src/model.c:132-361) with the repetition penalty.                  */
 /* ------------------------------------------------------------------ */
 typedef struct bm_hip_model bm_hip_model_t;
 
@@ -257,15 +257,28 @@ int bm_hip_model_reset(bm_hip_model_t *m);
 /* model_prefill (src/model.c:1045-1153): n tokens through every layer,
  * batched BitLinear + token-serial SSM; no LM head.  0 or -1. */
 int bm_hip_model_prefill(bm_hip_model_t *m, const int32_t *tokens, int n);
-/* model_forward_step with temp < 0.05 (src/model.c:1175-1314): returns the
- * greedy next token; history[history_len] as the reference's caller keeps
- * it (the last 256 tokens are used). */
+/* model_forward_step (src/model.c:1175-1314) with the sampler set by
+ * bm_hip_model_set_sampler: returns the next token; history[history_len]
+ * as the reference's caller keeps it (the last 256 tokens are used). */
 int bm_hip_model_step(bm_hip_model_t *m,
                       int token,
                       const int *history,
                       int history_len,
                       float penalty);
-/* copies the logits of the last step (after the penalty) */
+/* Sampling parameters of every later step, generate and decode: the
+ * temp, min_p, top_p, top_k arguments of model_forward_step
+ * (src/model.c:1175-1183), sampled on the device by sample_advanced
+ * (src/model.c:132-361).  temp < 0.05 is greedy (the default). */
+int bm_hip_model_set_sampler(bm_hip_model_t *m,
+                             float temp,
+                             float min_p,
+                             float top_p,
+                             int top_k);
+/* rng_seed (src/utils.c:121-124) for the model's device generator; the
+ * model starts with the reference's default state. */
+int bm_hip_model_seed(bm_hip_model_t *m, uint64_t seed);
+/* copies the logits of the last step (after the penalty; divided by the
+ * temperature when the step sampled, like the reference's) */
 int bm_hip_model_logits(const bm_hip_model_t *m, float *out);
 /* copies one layer's conv_state [3][d_inner] and ssm_state [d_inner];
  * returns the ring position */
@@ -274,7 +287,8 @@ int bm_hip_model_layer_state(const bm_hip_model_t *m,
                              float *conv_state,
                              float *ssm_state);
 /* The decode loop of src/main.c:443-500 on the device: prefill
- * prompt[0..n-2], history = prompt, then n_steps greedy steps from
+ * prompt[0..n-2], history = prompt, then n_steps steps (greedy or sampled,
+ * bm_hip_model_set_sampler) from
  * prompt[n-1], each step one replay of a captured hipGraph with no host
  * synchronization.  Writes the tokens; *decode_ms = device time of the
  * steps (prefill excluded, as the reference's tok/s).  Returns the number of
@@ -287,7 +301,7 @@ int bm_hip_model_generate(bm_hip_model_t *m,
                           int stop_on_eos,
                           int32_t *out_tokens,
                           double *decode_ms);
-/* n_steps more greedy steps from the current device state; tokens
+/* n_steps more steps from the current device state; tokens
  * readable with bm_hip_model_tokens. */
 int bm_hip_model_decode(bm_hip_model_t *m,
                         int n_steps,

@@ -29,6 +29,222 @@ uint64_t orc_rng_next(uint64_t *state)
 }
 
 /* ------------------------------------------------------------------ */
+/* Sampler (src/model.c:37-361): temperature, min_p, top_k (bucket      */
+/* histogram + min-heap), top_p, CDF draw                               */
+/* ------------------------------------------------------------------ */
+typedef struct {
+    int id;
+    float val;
+} orc_cand_t;
+
+/* descending by value; equal values compare equal (src/model.c:37-43) */
+static int orc_desc(const void *pa, const void *pb)
+{
+    const float d = ((const orc_cand_t *) pb)->val - ((const orc_cand_t *) pa)->val;
+    if (d > 0)
+        return 1;
+    return d < 0 ? -1 : 0;
+}
+
+/* min-heap on val: the node moves below the smaller child, the left one
+ * when both are smaller and equal (src/model.c:50-65) */
+static void orc_heap_down(orc_cand_t *h, int n, int i)
+{
+    for (;;) {
+        int m = i;
+        const int l = 2 * i + 1;
+        if (l < n && h[l].val < h[m].val)
+            m = l;
+        if (l + 1 < n && h[l + 1].val < h[m].val)
+            m = l + 1;
+        if (m == i)
+            return;
+        orc_cand_t t = h[i];
+        h[i] = h[m];
+        h[m] = t;
+        i = m;
+    }
+}
+
+/* keep the k largest of c[0..n) in c[0..k), heap-ordered (src/model.c:238-250) */
+static void orc_heap_keep(orc_cand_t *c, int n, int k)
+{
+    for (int i = k / 2 - 1; i >= 0; i--)
+        orc_heap_down(c, k, i);
+    for (int i = k; i < n; i++)
+        if (c[i].val > c[0].val) {
+            c[0] = c[i];
+            orc_heap_down(c, k, 0);
+        }
+}
+
+static float orc_uniform(uint64_t *rng)
+{
+    return (float) (orc_rng_next(rng) >> 11) * (1.0f / 9007199254740992.0f);
+}
+
+/* filter_and_sample with min_p = 0 (src/model.c:67-127) */
+static int orc_draw(const orc_cand_t *c, int n, float top_p, int top_k, uint64_t *rng)
+{
+    if (top_p < 1.0f) {
+        double acc = 0.0;
+        int i = 0;
+        while (i < n) {
+            acc += c[i].val;
+            i++;
+            if (acc >= top_p)
+                break;
+        }
+        n = i;
+    }
+    if (top_k > 0 && n > top_k)
+        n = top_k;
+    double total = 0.0;
+    for (int i = 0; i < n; i++)
+        total += c[i].val;
+    const float r = orc_uniform(rng) * (float) total;
+    double cdf = 0.0;
+    for (int i = 0; i < n; i++) {
+        cdf += c[i].val;
+        if (r < cdf)
+            return c[i].id;
+    }
+    return c[n - 1].id;
+}
+
+static int orc_first_max(const float *v, int n)
+{
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (v[i] > v[best])
+            best = i;
+    return best;
+}
+
+/* softmax of c[0..n) against `top`: expf(v - top), divided by the double
+ * sum taken in array order (src/model.c:253-266, 293-300) */
+static void orc_softmax(orc_cand_t *c, int n, float top)
+{
+    double z = 0.0;
+    for (int i = 0; i < n; i++) {
+        c[i].val = expf(c[i].val - top);
+        z += c[i].val;
+    }
+    const float inv = 1.0f / (float) z;
+    for (int i = 0; i < n; i++)
+        c[i].val *= inv;
+}
+
+int orc_sample(float *logits, int vocab, float temp, float min_p, float top_p, int top_k,
+               uint64_t *rng)
+{
+    if (temp < 0.05f) {
+        int best = 0;
+        float top = -1e9f;
+        for (int i = 0; i < vocab; i++)
+            if (logits[i] > top) {
+                top = logits[i];
+                best = i;
+            }
+        return best;
+    }
+    const float inv_t = 1.0f / temp;
+    float top = -1e30f;
+    for (int i = 0; i < vocab; i++) {
+        logits[i] *= inv_t;
+        if (logits[i] > top)
+            top = logits[i];
+    }
+    float floor_v = -1e30f;
+    if (min_p >= 1.0f)
+        floor_v = top;
+    else if (min_p > 0.0f)
+        floor_v = top + logf(min_p);
+
+    orc_cand_t *c = malloc((size_t) vocab * sizeof(*c));
+    int tok;
+    if (top_k > 0 && top_k <= 256) {
+        int count[128] = {0};
+        const float per_unit = 127.0f / 20.0f;
+        for (int i = 0; i < vocab; i++) {
+            if (!(logits[i] >= floor_v))
+                continue;
+            int b = (int) ((top - logits[i]) * per_unit);
+            b = b > 127 ? 127 : b;
+            b = b < 0 ? 0 : b;
+            count[b]++;
+        }
+        int cut = 127, seen = 0;
+        for (int b = 0; b < 128; b++) {
+            seen += count[b];
+            if (seen >= top_k) {
+                cut = b;
+                break;
+            }
+        }
+        float lo = top - (float) (cut + 1) / per_unit;
+        if (!(lo > floor_v))
+            lo = floor_v;
+        int n = 0;
+        for (int i = 0; i < vocab; i++)
+            if (logits[i] >= lo)
+                c[n++] = (orc_cand_t) {i, logits[i]};
+        if (n == 0) {
+            tok = orc_first_max(logits, vocab);
+        } else {
+            if (n > top_k) {
+                orc_heap_keep(c, n, top_k);
+                n = top_k;
+            }
+            float lm = -1e30f;
+            for (int i = 0; i < n; i++)
+                if (c[i].val > lm)
+                    lm = c[i].val;
+            orc_softmax(c, n, lm);
+            if (top_p < 1.0f)
+                qsort(c, n, sizeof(*c), orc_desc);
+            tok = orc_draw(c, n, top_p, 0, rng);
+        }
+    } else {
+        int n = 0;
+        for (int i = 0; i < vocab; i++)
+            if (logits[i] >= floor_v)
+                c[n++] = (orc_cand_t) {i, logits[i]};
+        if (n == 0) {
+            tok = orc_first_max(logits, vocab);
+        } else {
+            orc_softmax(c, n, top);
+            tok = -1;
+            if (top_p >= 1.0f && (top_k <= 0 || top_k >= n)) {
+                tok = orc_draw(c, n, top_p, top_k, rng);
+            } else {
+                if (top_p < 1.0f && n > 256) {
+                    orc_cand_t part[256];
+                    orc_cand_t *tmp = malloc((size_t) n * sizeof(*tmp));
+                    memcpy(tmp, c, (size_t) n * sizeof(*tmp));
+                    orc_heap_keep(tmp, n, 256);
+                    memcpy(part, tmp, sizeof(part));
+                    free(tmp);
+                    qsort(part, 256, sizeof(part[0]), orc_desc);
+                    double acc = 0.0;
+                    for (int i = 0; i < 256 && tok < 0; i++) {
+                        acc += part[i].val;
+                        if (acc >= top_p)
+                            tok = orc_draw(part, 256, top_p, top_k, rng);
+                    }
+                }
+                if (tok < 0) {
+                    qsort(c, n, sizeof(*c), orc_desc);
+                    tok = orc_draw(c, n, top_p, top_k, rng);
+                }
+            }
+        }
+    }
+    free(c);
+    return tok;
+}
+
+/* ------------------------------------------------------------------ */
 /* a1: ternary decode tables (src/quantization.c:12-53)                 */
 /* ------------------------------------------------------------------ */
 int orc_decode_weight(int bits)

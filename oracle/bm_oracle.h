@@ -21,6 +21,12 @@
  *   orc_model_*                    bit-exact logits + identical greedy
  *                                  streams vs _ref model_load/prefill/
  *                                  forward_step on synthetic BIT2 files
+ *   orc_sample                     identical draws vs _ref model_forward_step
+ *                                  sampling the same logits from the same
+ *                                  generator state, on every path (top-k
+ *                                  heap, top-p partial and full sort,
+ *                                  min_p, greedy); closed forms: min_p = 1
+ *                                  keeps only the max, top_k = 1 is greedy
  * No function is left unpinned.
  */
 #pragma once
@@ -34,6 +40,10 @@ extern "C" {
 
 /* XorShift64* (src/utils.c:117-140), with the state passed explicitly. */
 uint64_t orc_rng_next(uint64_t *state);
+/* sample_advanced (src/model.c:132-361) with filter_and_sample: returns the
+ * drawn token; logits are scaled by 1/temp in place like the reference's */
+int orc_sample(float *logits, int vocab, float temp, float min_p, float top_p, int top_k,
+               uint64_t *rng);
 
 /* 2-bit code -> {-1, 0, +1, +1} (src/quantization.c:27-31). */
 int orc_decode_weight(int bits);

@@ -218,6 +218,22 @@ int bmref_model_step(void *h,
                               history_len, penalty, 0.0f, 0.0f, 1.0f, 0);
 }
 
+/* model_forward_step with the reference's sampler (temp >= 0.05 samples
+ * with the global generator seeded by bmref_rng_seed). */
+int bmref_model_step_sample(void *h,
+                            int token,
+                            const int *history,
+                            int history_len,
+                            float penalty,
+                            float temp,
+                            float min_p,
+                            float top_p,
+                            int top_k)
+{
+    return model_forward_step((bitmamba_model_t *) h, token, history,
+                              history_len, penalty, temp, min_p, top_p, top_k);
+}
+
 const float *bmref_model_logits(void *h)
 {
     return ((bitmamba_model_t *) h)->logits;

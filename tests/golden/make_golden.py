@@ -125,19 +125,70 @@ def make_stream(R, name, threads):
     print(name, "done in %.1fs" % (time.time() - t0), toks[:16])
 
 
+# sampled decoding: (temp, min_p, top_p, top_k, penalty, seed), each branch
+# of sample_advanced (src/model.c:132-361) on this model's logits
+SAMPLE = dict(model=dict(vocab=5000, d_model=128, n_layers=2, n_heads=4, dist=0, seed=21,
+                         prompt=8, steps=24),
+              cases=[(0.8, 0.05, 0.9, 40, 1.0, 42), (1.0, 0.0, 1.0, 40, 1.0, 7),
+                     (1.2, 0.0, 0.95, 256, 1.3, 9), (0.7, 0.0, 0.9, 0, 1.0, 11),
+                     (10.0, 0.0, 0.99, 0, 1.0, 13), (1.0, 0.1, 1.0, 0, 1.0, 17),
+                     (10.0, 0.0, 1.0, 300, 1.0, 19), (1.0, 1.0, 1.0, 0, 1.0, 23),
+                     (0.9, 0.0, 1.0, 1, 1.0, 29), (0.01, 0.0, 1.0, 0, 1.0, 31)])
+
+
+def make_sample_streams(R, threads):
+    c = SAMPLE["model"]
+    t0 = time.time()
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          c["dist"])
+    prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
+    streams = []
+    with tempfile.NamedTemporaryFile(suffix=".bin", dir="/tmp") as f:
+        blob.tofile(f.name)
+        R.bmref_init(threads, 0)
+        for case in SAMPLE["cases"]:
+            temp, min_p, top_p, top_k, penalty, seed = case
+            h = R.bmref_model_load(f.name.encode())
+            assert h, "reference model_load rejected the synthetic image"
+            p = np.ascontiguousarray(prompt[:-1], np.int32)
+            R.bmref_model_prefill(h, ptr(p), len(p))
+            R.bmref_rng_seed(seed)
+            hist, cur, toks = [int(t) for t in prompt], int(prompt[-1]), []
+            for _ in range(c["steps"]):
+                harr = np.array(hist[-256:], np.int32)
+                cur = R.bmref_model_step_sample(h, cur, ptr(harr), len(harr), penalty, temp,
+                                                min_p, top_p, top_k)
+                toks.append(int(cur))
+                hist.append(cur)
+            R.bmref_model_free(h)
+            streams.append(dict(temp=temp, min_p=min_p, top_p=top_p, top_k=top_k,
+                                penalty=penalty, seed=seed, tokens=toks))
+    rec = dict(config=c, blob_bytes=int(blob.nbytes), blob_sha256=sha(blob),
+               prompt=[int(t) for t in prompt], streams=streams,
+               generator="reference scalar kernels + sample_advanced (oracle/_ref, %d threads)"
+                         % threads,
+               seconds=round(time.time() - t0, 1))
+    with open(os.path.join(HERE, "stream_sample.json"), "w") as f:
+        json.dump(rec, f, indent=1)
+    print("sample streams done in %.1fs" % (time.time() - t0))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--skip-1b", action="store_true")
+    ap.add_argument("--only-sample", action="store_true")
     ap.add_argument("--threads", type=int, default=8)
     a = ap.parse_args()
     if not native.ref_available():
         sys.exit("oracle/_ref/libbmref.so is not built")
     R = native.ref()
     R.bmref_init(1, 0)
-    make_quant(R)
-    make_bitlinear(R)
-    for name in ("tiny", "255m") + (() if a.skip_1b else ("1b",)):
-        make_stream(R, name, a.threads)
+    if not a.only_sample:
+        make_quant(R)
+        make_bitlinear(R)
+        for name in ("tiny", "255m") + (() if a.skip_1b else ("1b",)):
+            make_stream(R, name, a.threads)
+    make_sample_streams(R, a.threads)
     R.bmref_shutdown()
 
 

@@ -31,6 +31,7 @@ def ptr(a):
 
 _ORACLE_SIGS = {
     "orc_rng_next": (_u64, [C.POINTER(_u64)]),
+    "orc_sample": (_i, [_vp, _i, _f, _f, _f, _i, C.POINTER(_u64)]),
     "orc_decode_weight": (_i, [_i]),
     "orc_luts": (None, [_vp, _vp, _vp]),
     "orc_rms_norm": (_f, [_vp, _i, _vp, _vp]),
@@ -73,6 +74,7 @@ _REF_SIGS = {
     "bmref_model_free": (None, [_vp]),
     "bmref_model_prefill": (None, [_vp, _vp, _i]),
     "bmref_model_step": (_i, [_vp, _i, _vp, _i, _f]),
+    "bmref_model_step_sample": (_i, [_vp, _i, _vp, _i, _f, _f, _f, _f, _i]),
     "bmref_model_logits": (C.POINTER(C.c_float), [_vp]),
     "bmref_model_vocab": (_i, [_vp]),
     "bmref_model_layer_state": (_i, [_vp, _i, _vp, _vp]),

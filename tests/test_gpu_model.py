@@ -139,3 +139,71 @@ def test_255m_stream_matches_reference(hip):
 
 def test_1b_stream_matches_reference(hip):
     _stream_check(hip, "1b")
+
+
+def _sample_fixture():
+    with open(os.path.join(GOLD, "stream_sample.json")) as f:
+        g = json.load(f)
+    c = g["config"]
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          c["dist"])
+    assert blob.nbytes == g["blob_bytes"]
+    return g, blob, np.array(g["prompt"], np.int32), c["steps"]
+
+
+def test_sampled_streams_match_reference(hip):
+    """Device sampler (every branch of sample_advanced, the repetition
+    penalty, greedy below temp 0.05) against the reference's own sampled
+    streams (tests/golden/stream_sample.json), each case from a reset model
+    and a freshly seeded generator, as one captured graph per step."""
+    g, blob, prompt, steps = _sample_fixture()
+    m = bh.Model(blob)
+    try:
+        for s in g["streams"]:
+            note("sampled stream temp=%g min_p=%g top_p=%g top_k=%d penalty=%g seed=%d"
+                 % (s["temp"], s["min_p"], s["top_p"], s["top_k"], s["penalty"], s["seed"]))
+            m.reset()
+            m.set_sampler(s["temp"], s["min_p"], s["top_p"], s["top_k"])
+            m.seed(s["seed"])
+            toks, _ = m.generate(prompt, steps, s["penalty"])
+            assert [int(t) for t in toks] == s["tokens"], s
+    finally:
+        m.free()
+
+
+def test_sampled_steps_logits_vs_oracle(hip):
+    """bm_hip_model_step with the sampler: each step's token and its logits
+    (penalty applied, divided by the temperature in place as the reference
+    leaves them) bit-exact against the oracle model + orc_sample."""
+    g, blob, prompt, steps = _sample_fixture()
+    O, h = _oracle_model(blob)
+    m = bh.Model(blob)
+    try:
+        for s in (g["streams"][2], g["streams"][4]):
+            note("sampled steps temp=%g top_k=%d penalty=%g" % (s["temp"], s["top_k"],
+                                                                s["penalty"]))
+            m.reset()
+            O.orc_model_free(h)
+            h = O.orc_model_load(ptr(blob), blob.nbytes)
+            p = prompt[:-1].copy()
+            m.prefill(p)
+            O.orc_model_prefill(h, ptr(p), p.size)
+            m.set_sampler(s["temp"], s["min_p"], s["top_p"], s["top_k"])
+            m.seed(s["seed"])
+            rng = native.C.c_uint64(s["seed"])
+            V = O.orc_model_config(h, 0)
+            hist, cur = [int(t) for t in prompt], int(prompt[-1])
+            for i in range(8):
+                harr = np.array(hist[-256:], np.int32)
+                t_dev = m.step(cur, harr, s["penalty"])
+                O.orc_model_step(h, cur, ptr(harr), harr.size, s["penalty"])
+                lg = np.ctypeslib.as_array(O.orc_model_logits(h), (V,)).copy()
+                t_orc = O.orc_sample(ptr(lg), V, s["temp"], s["min_p"], s["top_p"], s["top_k"],
+                                     native.C.byref(rng))
+                assert t_dev == t_orc == s["tokens"][i], (i, s)
+                same_bits(m.logits(), lg, "scaled logits")
+                hist.append(t_dev)
+                cur = t_dev
+    finally:
+        m.free()
+        O.orc_model_free(h)

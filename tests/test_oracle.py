@@ -6,6 +6,8 @@
 * against invariants the scalar path must satisfy (scale invariance of the
   int8 vector, the largest element quantizing to +-127, ties away from zero).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -270,3 +272,105 @@ def test_model_loader_rejects_malformed():
     assert not O.orc_model_load(ptr(bad), bad.nbytes)
     trunc = blob[: blob.nbytes // 2].copy()
     assert not O.orc_model_load(ptr(trunc), trunc.nbytes)
+
+
+# --------------------------------------------------- sampler
+# (temp, min_p, top_p, top_k, penalty, seed): every branch of
+# sample_advanced (src/model.c:132-361) on the tiny model's logits
+SAMPLER_CASES = [
+    (0.8, 0.05, 0.9, 40, 1.0, 42),    # top-k heap, sorted for top_p
+    (1.0, 0.0, 1.0, 40, 1.0, 7),      # top-k heap, CDF in heap order
+    (1.2, 0.0, 0.95, 256, 1.3, 9),    # k = 256 with the repetition penalty
+    (0.7, 0.0, 0.9, 0, 1.0, 11),      # no top-k: top-256 partial sort
+    (10.0, 0.0, 0.99, 0, 1.0, 13),    # flat: the partial sort falls short, full sort
+    (1.0, 0.1, 1.0, 0, 1.0, 17),      # min_p, CDF in index order
+    (10.0, 0.0, 1.0, 300, 1.0, 19),   # top_k > 256: full sort, then top_k
+    (1.0, 1.0, 1.0, 0, 1.0, 23),      # min_p = 1: only the maximum survives
+    (0.9, 0.0, 1.0, 1, 1.0, 29),      # top_k = 1
+    (0.01, 0.0, 1.0, 0, 1.0, 31),     # temp < 0.05: greedy
+]
+SAMPLER_MODEL = dict(vocab=5000, d_model=128, n_layers=2, n_heads=4, seed=21)
+
+
+def sampler_model():
+    c = SAMPLER_MODEL
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          bh.SYNTH_UNIFORM)
+    return blob, bh.synth_prompt(c["seed"], c["vocab"], 8)
+
+
+def sampler_branch(logits, temp, min_p, top_p, top_k):
+    """Which branch of sample_advanced these logits take (numpy, float32
+    like the reference); used to show the cases cover all of them."""
+    if temp < 0.05:
+        return "greedy"
+    z = (logits * np.float32(1.0 / np.float32(temp))).astype(np.float32)
+    mx = z.max()
+    thr = np.float32(-1e30)
+    if min_p >= 1.0:
+        thr = mx
+    elif min_p > 0.0:
+        thr = np.float32(mx + np.float32(np.log(np.float32(min_p))))
+    if 0 < top_k <= 256:
+        return "topk_heap" if (z >= thr).sum() > top_k else "topk"
+    n = int((z >= thr).sum())
+    if top_p >= 1.0 and (top_k <= 0 or top_k >= n):
+        return "direct"
+    if top_p < 1.0 and n > 256:
+        p = np.exp((z[z >= thr] - mx).astype(np.float64))
+        p /= p.sum()
+        return "partial" if np.sort(p)[::-1][:256].sum() >= top_p * (1 - 1e-6) else "full"
+    return "full"
+
+
+def sampler_ref_stream(ref_lib, path, prompt, steps, case):
+    """The reference's sampled stream with, in lockstep, a greedy instance
+    that exposes the logits each draw sees."""
+    temp, min_p, top_p, top_k, penalty, seed = case
+    hs = ref_lib.bmref_model_load(path.encode())
+    hg = ref_lib.bmref_model_load(path.encode())
+    assert hs and hg
+    try:
+        p = np.ascontiguousarray(prompt[:-1], np.int32)
+        ref_lib.bmref_model_prefill(hs, ptr(p), len(p))
+        ref_lib.bmref_model_prefill(hg, ptr(p), len(p))
+        ref_lib.bmref_rng_seed(seed)
+        V = ref_lib.bmref_model_vocab(hs)
+        hist, cur = list(prompt), int(prompt[-1])
+        toks, seen = [], []
+        for _ in range(steps):
+            harr = np.array(hist[-256:], np.int32)
+            ref_lib.bmref_model_step(hg, cur, ptr(harr), len(harr), penalty)
+            seen.append(np.ctypeslib.as_array(ref_lib.bmref_model_logits(hg), (V,)).copy())
+            cur = ref_lib.bmref_model_step_sample(hs, cur, ptr(harr), len(harr), penalty, temp,
+                                                  min_p, top_p, top_k)
+            toks.append(cur)
+            hist.append(cur)
+        return toks, seen
+    finally:
+        ref_lib.bmref_model_free(hs)
+        ref_lib.bmref_model_free(hg)
+
+
+def test_sampler_vs_reference(ref_lib, tmp_path):
+    """orc_sample draws the reference's token from the same logits and
+    generator state on every branch; min_p = 1 and top_k = 1 reduce to the
+    first maximum."""
+    ref_lib.bmref_init(2, 0)
+    blob, prompt = sampler_model()
+    path = tmp_path / "s.bin"
+    blob.tofile(path)
+    O = native.oracle()
+    branches = set()
+    for case in SAMPLER_CASES:
+        temp, min_p, top_p, top_k, penalty, seed = case
+        toks, seen = sampler_ref_stream(ref_lib, str(path), prompt, 16, case)
+        rng = C.c_uint64(seed if seed else 0x853C49E6748FEA9B)
+        for t, lg in zip(toks, seen):
+            branches.add(sampler_branch(lg, temp, min_p, top_p, top_k))
+            work = lg.copy()
+            got = O.orc_sample(ptr(work), lg.size, temp, min_p, top_p, top_k, C.byref(rng))
+            assert got == t, case
+            if min_p >= 1.0 or top_k == 1 or temp < 0.05:
+                assert t == int(np.argmax(lg)), case
+    assert branches >= {"greedy", "topk", "topk_heap", "direct", "partial", "full"}, branches
