@@ -10,6 +10,8 @@ one replay of the captured per-token hipGraph with inputs already in HBM.
 Prints ONE JSON line.  Legs (all by default):
   decode    W untimed steps, then K timed steps -> tok/s (the value) and
             packed-weight GB/s
+  sampled   the same model decoding with the device sampler (temp 0.8,
+            min_p 0.05, top_p 0.9, top_k 40): tok/s of up to 128 steps
   roofline  the decode GEMV kernel (K=2048 in_proj shape) streaming 512 MiB
             of distinct weight rows in one launch, timed with HIP events on
             the library stream -> achieved GB/s vs 8 TB/s
@@ -80,7 +82,10 @@ class Events:
         return self.L.bm_hip_event_elapsed_ms(self.a, self.b)
 
 
-def leg_decode(L, steps, warmup):
+SAMPLED = dict(temp=0.8, min_p=0.05, top_p=0.9, top_k=40, seed=42)
+
+
+def leg_decode(L, steps, warmup, sampled=False):
     c = CFG_1B
     t0 = time.time()
     blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
@@ -96,6 +101,21 @@ def leg_decode(L, steps, warmup):
     L.bm_hip_synchronize()
     wall = time.perf_counter() - t0
     toks = np.concatenate([first, m.tokens(steps)])
+    samp = None
+    if sampled:
+        # the same model and prompt with the device sampler
+        m.reset()
+        m.set_sampler(SAMPLED["temp"], SAMPLED["min_p"], SAMPLED["top_p"], SAMPLED["top_k"])
+        m.seed(SAMPLED["seed"])
+        m.generate(prompt, warmup)
+        L.bm_hip_synchronize()
+        n = min(steps, 128)
+        t1 = time.perf_counter()
+        sms = m.decode(n)
+        L.bm_hip_synchronize()
+        sw = time.perf_counter() - t1
+        samp = dict(SAMPLED, steps=n, tok_s=round(n / sw, 2), ms_per_step=round(sw * 1e3 / n, 4),
+                    device_ms_per_step=round(sms / n, 4))
     m.free()
     match = None
     gold = os.path.join(ROOT, "tests", "golden", "stream_1b.json")
@@ -103,7 +123,7 @@ def leg_decode(L, steps, warmup):
         ref = json.load(open(gold))["tokens"]
         n = min(len(ref), len(toks))
         match = toks[:n].tolist() == ref[:n]
-    return wall, dev_ms, match
+    return wall, dev_ms, match, samp
 
 
 def leg_d255m(L):
@@ -459,7 +479,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--legs", default="decode,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
+    ap.add_argument("--legs",
+                    default="decode,sampled,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (the BitLinear hot path at bs=1 "
@@ -471,9 +492,12 @@ def main():
         sys.exit("bm_hip_init: " + bh.last_error())
     res = {}
     if "decode" in legs:
-        wall, dev_ms, match = leg_decode(L, a.steps, a.warmup)
+        wall, dev_ms, match, samp = leg_decode(L, a.steps, a.warmup, "sampled" in legs)
         res["decode"] = (wall, dev_ms, match)
+        res["sampled"] = samp
         log("decode: %d steps in %.2f ms wall (%.2f ms device)" % (a.steps, wall * 1e3, dev_ms))
+        if samp:
+            log("sampled decode: %s" % json.dumps(samp))
     roof = leg_roofline(L) if "roofline" in legs else None
     if roof:
         log("roofline: %.1f GB/s (%.1f%% of HBM peak), %.1f us per launch"
@@ -521,6 +545,7 @@ def main():
                     tokens_match_reference=match)
     else:
         line.update(value=None, ms_per_step=None)
+    line["decode_sampled"] = res.get("sampled")
     line["roofline"] = roof
     line["mfma_ceiling"] = mf
     line["prefill_gemm"] = pre
