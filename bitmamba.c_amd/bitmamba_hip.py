@@ -80,6 +80,9 @@ SIGNATURES = {
     "bm_hip_model_step": (_i, [_vp, _i, _vp, _i, _f]),
     "bm_hip_model_set_sampler": (_i, [_vp, _f, _f, _f, _i]),
     "bm_hip_model_seed": (_i, [_vp, _u64]),
+    "bm_hip_model_state_bytes": (_sz, [_vp]),
+    "bm_hip_model_state_save": (_i, [_vp, _vp, _sz]),
+    "bm_hip_model_state_load": (_i, [_vp, _vp, _sz]),
     "bm_hip_model_logits": (_i, [_vp, _vp]),
     "bm_hip_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
     "bm_hip_model_generate": (_i, [_vp, _vp, _i, _i, _f, _i, _vp, C.POINTER(C.c_double)]),
@@ -261,6 +264,19 @@ class Model:
 
     def seed(self, seed):
         check(lib().bm_hip_model_seed(self.h, seed), "seed")
+
+    def state_save(self):
+        """The recurrent state as a BMST image (bytes)."""
+        n = lib().bm_hip_model_state_bytes(self.h)
+        buf = np.empty(n, np.uint8)
+        if lib().bm_hip_model_state_save(self.h, ptr(buf), n) != n:
+            raise RuntimeError("state_save: " + last_error())
+        return buf.tobytes()
+
+    def state_load(self, image):
+        """Loads a BMST image; False (with bm_hip_last_error) if rejected."""
+        buf = np.frombuffer(image, np.uint8).copy()
+        return lib().bm_hip_model_state_load(self.h, ptr(buf), buf.size) == 0
 
     def logits(self):
         out = np.empty(self.vocab, np.float32)

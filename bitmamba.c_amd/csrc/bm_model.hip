@@ -712,6 +712,99 @@ extern "C" int bm_hip_model_seed(bm_hip_model_t* m, uint64_t seed) {
   return 0;
 }
 
+// --- recurrent state files (state_save / state_load, src/chat.c:1160-1271) ---
+// BMST image: u32 magic "BMST", n_layers, d_inner, d_conv; then per layer
+// conv_state [(d_conv-1) * d_inner] floats, ssm_state [d_inner] floats and
+// the int conv_pos.  The device model keeps one ring position for all
+// layers (they advance together), so an image whose layers disagree on it is
+// rejected.
+namespace {
+constexpr uint32_t kStateMagic = 0x424D5354;  // src/chat.h:14-15
+constexpr int kDConv = 4;                     // BM_CONV_KERNEL
+}  // namespace
+
+extern "C" size_t bm_hip_model_state_bytes(const bm_hip_model_t* m) {
+  return 16 + (size_t)m->nl * ((size_t)(kDConv - 1) * m->di * 4 + (size_t)m->di * 4 + 4);
+}
+
+extern "C" int bm_hip_model_state_save(const bm_hip_model_t* m, void* out, size_t len) {
+  const size_t need = bm_hip_model_state_bytes(m);
+  if (!out || len < need) {
+    bm_set_error("state_save: buffer of %zu bytes, %zu needed", len, need);
+    return -1;
+  }
+  const size_t conv = (size_t)(kDConv - 1) * m->di, lay = conv * 4 + (size_t)m->di * 4 + 4;
+  std::vector<float> cs((size_t)m->nl * conv), ss((size_t)m->nl * m->di);
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipStreamSynchronize(m->stream));
+  MCHECK(hipMemcpy(cs.data(), m->conv_state, cs.size() * 4, hipMemcpyDeviceToHost));
+  MCHECK(hipMemcpy(ss.data(), m->ssm_state, ss.size() * 4, hipMemcpyDeviceToHost));
+  MCHECK(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
+  uint8_t* p = (uint8_t*)out;
+  const uint32_t hdr[4] = {kStateMagic, (uint32_t)m->nl, (uint32_t)m->di, (uint32_t)kDConv};
+  memcpy(p, hdr, 16);
+  for (int l = 0; l < m->nl; ++l) {
+    uint8_t* q = p + 16 + (size_t)l * lay;
+    memcpy(q, cs.data() + (size_t)l * conv, conv * 4);
+    memcpy(q + conv * 4, ss.data() + (size_t)l * m->di, (size_t)m->di * 4);
+    memcpy(q + conv * 4 + (size_t)m->di * 4, &ctl[bm::CTL_POS], 4);
+  }
+  return (int)need;
+}
+
+extern "C" int bm_hip_model_state_load(bm_hip_model_t* m, const void* in, size_t len) {
+  const uint8_t* p = (const uint8_t*)in;
+  uint32_t hdr[4];
+  if (!in || len < 16) {
+    bm_set_error("state_load: short header");
+    return -1;
+  }
+  memcpy(hdr, p, 16);
+  if (hdr[0] != kStateMagic) {
+    bm_set_error("state_load: invalid magic");
+    return -1;
+  }
+  if ((int)hdr[1] != m->nl || (int)hdr[2] != m->di || (int)hdr[3] != kDConv) {
+    bm_set_error("state_load: dimensions mismatch (layers=%u/%d, d_inner=%u/%d, d_conv=%u/%d)",
+                 hdr[1], m->nl, hdr[2], m->di, hdr[3], kDConv);
+    return -1;
+  }
+  const size_t conv = (size_t)(kDConv - 1) * m->di, lay = conv * 4 + (size_t)m->di * 4 + 4;
+  std::vector<float> cs((size_t)m->nl * conv), ss((size_t)m->nl * m->di);
+  int pos = -1;
+  const char* why = nullptr;
+  for (int l = 0; l < m->nl && !why; ++l) {
+    if (16 + (size_t)(l + 1) * lay > len) {
+      why = "truncated";
+      break;
+    }
+    const uint8_t* q = p + 16 + (size_t)l * lay;
+    memcpy(cs.data() + (size_t)l * conv, q, conv * 4);
+    memcpy(ss.data() + (size_t)l * m->di, q + conv * 4, (size_t)m->di * 4);
+    int cp;
+    memcpy(&cp, q + conv * 4 + (size_t)m->di * 4, 4);
+    if (cp < 0 || cp >= kDConv - 1)
+      why = "invalid conv_pos";
+    else if (l > 0 && cp != pos)
+      why = "layers at different conv positions";
+    pos = cp;
+  }
+  if (why) {
+    // the reference resets the state after a bad layer (src/chat.c:1246-1265)
+    bm_set_error("state_load: %s", why);
+    if (bm_hip_model_reset(m)) return -1;
+    return -1;
+  }
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipStreamSynchronize(m->stream));
+  MCHECK(hipMemcpy(m->conv_state, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  MCHECK(hipMemcpy(m->ssm_state, ss.data(), ss.size() * 4, hipMemcpyHostToDevice));
+  MCHECK(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
+  ctl[bm::CTL_POS] = pos;
+  MCHECK(hipMemcpy(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice));
+  return 0;
+}
+
 extern "C" int bm_hip_model_logits(const bm_hip_model_t* m, float* out) {
   MCHECK(hipMemcpyAsync(out, m->logits, (size_t)m->vocab * 4, hipMemcpyDeviceToHost, m->stream));
   MCHECK(hipStreamSynchronize(m->stream));

@@ -277,6 +277,18 @@ int bm_hip_model_set_sampler(bm_hip_model_t *m,
 /* rng_seed (src/utils.c:121-124) for the model's device generator; the
  * model starts with the reference's default state. */
 int bm_hip_model_seed(bm_hip_model_t *m, uint64_t seed);
+/* Recurrent state as a BMST image (state_save / state_load,
+ * src/chat.c:1160-1271): u32 magic 0x424D5354, n_layers, d_inner, d_conv,
+ * then per layer conv_state[(d_conv-1)*d_inner], ssm_state[d_inner] (fp32)
+ * and conv_pos (int).  File I/O stays with the caller.  save returns the
+ * bytes written (bm_hip_model_state_bytes) or -1; load returns 0, or -1
+ * leaving the state untouched on a bad magic or dimensions and reset to
+ * zero on a truncated image or a bad ring position, as the reference does.
+ * Layers at different ring positions are rejected (the device model keeps
+ * one position; the reference's layers always share it). */
+size_t bm_hip_model_state_bytes(const bm_hip_model_t *m);
+int bm_hip_model_state_save(const bm_hip_model_t *m, void *out, size_t len);
+int bm_hip_model_state_load(bm_hip_model_t *m, const void *in, size_t len);
 /* copies the logits of the last step (after the penalty; divided by the
  * temperature when the step sampled, like the reference's) */
 int bm_hip_model_logits(const bm_hip_model_t *m, float *out);

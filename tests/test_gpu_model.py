@@ -207,3 +207,71 @@ def test_sampled_steps_logits_vs_oracle(hip):
     finally:
         m.free()
         O.orc_model_free(h)
+
+
+def _bmst(layers, pos, d_inner):
+    """A BMST image as src/chat.c:1160-1207 writes it: magic, n_layers,
+    d_inner, d_conv, then per layer conv_state, ssm_state, conv_pos."""
+    parts = [np.array([0x424D5354, len(layers), d_inner, 4], np.uint32).tobytes()]
+    for cs, ss in layers:
+        parts += [np.ascontiguousarray(cs, np.float32).tobytes(),
+                  np.ascontiguousarray(ss, np.float32).tobytes(), np.int32(pos).tobytes()]
+    return b"".join(parts)
+
+
+def test_state_save_load(hip):
+    """BMST images: the device's saved state equals the image built from the
+    oracle's state after the same tokens; a device model loaded from the
+    oracle's image continues with bit-exact logits; bad images are rejected
+    with the reference's outcome (untouched on a bad magic or dimensions,
+    reset on a truncated image or a bad ring position)."""
+    g = gold("tiny")
+    blob, prompt, _ = model_image(g)
+    note("BMST save/load")
+    O, h = _oracle_model(blob)
+    m = bh.Model(blob)
+    m2 = bh.Model(blob)
+    try:
+        p = prompt[:-1].copy()
+        m.prefill(p)
+        O.orc_model_prefill(h, ptr(p), p.size)
+        hist, cur = [int(t) for t in prompt], int(prompt[-1])
+        for _ in range(5):
+            harr = np.array(hist[-256:], np.int32)
+            cur = m.step(cur, harr)
+            assert cur == O.orc_model_step(h, hist[-1], ptr(harr), harr.size, 1.0)
+            hist.append(cur)
+        nl, di = m.n_layers, m.d_inner
+        layers, pos = [], None
+        for layer in range(nl):
+            cs = np.empty((3, di), np.float32)
+            ss = np.empty(di, np.float32)
+            pos = O.orc_model_layer_state(h, layer, ptr(cs), ptr(ss))
+            layers.append((cs, ss))
+        image = _bmst(layers, pos, di)
+        assert m.state_save() == image
+        # a fresh model continues from the oracle's image
+        assert m2.state_load(image)
+        for _ in range(4):
+            harr = np.array(hist[-256:], np.int32)
+            t2 = m2.step(cur, harr)
+            t_o = O.orc_model_step(h, cur, ptr(harr), harr.size, 1.0)
+            V = O.orc_model_config(h, 0)
+            same_bits(m2.logits(), np.ctypeslib.as_array(O.orc_model_logits(h), (V,)), "logits")
+            assert t2 == t_o
+            hist.append(t2)
+            cur = t2
+        saved = m2.state_save()
+        zero = _bmst([(np.zeros((3, di)), np.zeros(di))] * nl, 0, di)
+        bad_magic = b"XXXX" + saved[4:]
+        bad_dims = np.array([0x424D5354, nl + 1, di, 4], np.uint32).tobytes() + saved[16:]
+        bad_pos = _bmst(layers, 3, di)
+        for img, outcome in ((bad_magic, saved), (bad_dims, saved), (saved[:-5], zero),
+                             (bad_pos, zero)):
+            assert m2.state_load(saved)
+            assert not m2.state_load(img)
+            assert m2.state_save() == outcome
+    finally:
+        m.free()
+        m2.free()
+        O.orc_model_free(h)
