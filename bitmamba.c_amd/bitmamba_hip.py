@@ -80,6 +80,8 @@ SIGNATURES = {
     "bm_hip_model_step": (_i, [_vp, _i, _vp, _i, _f]),
     "bm_hip_model_set_sampler": (_i, [_vp, _f, _f, _f, _i]),
     "bm_hip_model_seed": (_i, [_vp, _u64]),
+    "bm_hip_sample_workspace_bytes": (_sz, [_i]),
+    "bm_hip_sample_advanced": (_i, [_vp, _i, _f, _f, _f, _i, _vp, _vp, _vp, _vp]),
     "bm_hip_model_state_bytes": (_sz, [_vp]),
     "bm_hip_model_state_save": (_i, [_vp, _vp, _sz]),
     "bm_hip_model_state_load": (_i, [_vp, _vp, _sz]),
@@ -209,6 +211,28 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+def sample_advanced(logits, temp, min_p=0.0, top_p=1.0, top_k=0, rng=0x853c49e6748fea9b):
+    """sample_advanced (src/model.c:132-361) on the device for host logits:
+    returns (token, the logits as the sampler leaves them, the next
+    XorShift64* state)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    V = lg.size
+    L = lib()
+    bl = DeviceBuffer.from_array(lg)
+    br = DeviceBuffer.from_array(np.array([rng], np.uint64))
+    bw = DeviceBuffer(L.bm_hip_sample_workspace_bytes(V))
+    bt = DeviceBuffer(4)
+    try:
+        check(L.bm_hip_sample_advanced(bl.ptr, V, temp, min_p, top_p, top_k, br.ptr, bw.ptr,
+                                       bt.ptr, L.bm_hip_stream()), "sample_advanced")
+        check(L.bm_hip_synchronize(), "synchronize")
+        return (int(bt.download((1,), np.int32)[0]), bl.download((V,), np.float32),
+                int(br.download((1,), np.uint64)[0]))
+    finally:
+        for b in (bl, br, bw, bt):
+            b.free()
 
 
 def make_tensor(packed=None, rows=0, cols=0, scale=1.0, data=None):

@@ -389,16 +389,19 @@ __device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32
 //   PRENORM: the input first goes through RMSNorm(gamma_pre) -- the
 //            reference's final norm -- then the BitLinear's own norm
 //   MODE:    0 store, 1 accumulate (residual)
-//   PICK:    each block also writes its first-max row (value, index)
+//   PICK:    1: each block also writes its first-max row (value, index);
+//            2: the rows are stored multiplied by 1/temp (the sampler's
+//               temperature, src/model.c:160-166) and each block writes the
+//               max of what it stored under `x > m` from -1e30f
 // ---------------------------------------------------------------------------
-template <int T, int P, int NPF, int C, bool PRENORM, int MODE, bool PICK, bool WP>
+template <int T, int P, int NPF, int C, bool PRENORM, int MODE, int PICK, bool WP>
 __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma_pre,
                                                     const float* __restrict__ gamma,
                                                     const uint8_t* __restrict__ W, int N,
                                                     float w_scale, float* __restrict__ out,
                                                     float* __restrict__ part_v,
-                                                    int* __restrict__ part_i) {
+                                                    int* __restrict__ part_i, float temp) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int RPW = 64 / T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -453,10 +456,12 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   int xsl[P];
   load_lane_act<P, T>(l, K, u, xa, xsl);
 
-  float best_v = -1e9f;
+  float best_v = PICK == 2 ? -1e30f : -1e9f;
   int best_i = 0x7fffffff;
+  const float inv_temp = PICK == 2 ? cr_divf(1.0f, temp) : 1.0f;
   auto emit = [&](int r, float o) {
     if (u == 0 && r < N) {
+      if (PICK == 2) o = __fmul_rn(o, inv_temp);
       if (MODE == 1)
         out[r] = __fadd_rn(out[r], o);
       else
@@ -491,7 +496,20 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
     emit(r, o);
   }
 
-  if constexpr (PICK) {
+  if constexpr (PICK == 2) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(best_v, o, 64);
+      if (ov > best_v) best_v = ov;
+    }
+    if (lane == 0) l.bc[16 + wave] = best_v;
+    __syncthreads();
+    if (tid == 0) {
+      for (int k = 1; k < 4; ++k)
+        if (l.bc[16 + k] > best_v) best_v = l.bc[16 + k];
+      part_v[blockIdx.x] = best_v;
+    }
+  } else if constexpr (PICK == 1) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
       const float ov = __shfl_xor(best_v, o, 64);
@@ -754,34 +772,34 @@ static int rows_blocks(int N, int K) {
   return b < 1 ? 1 : b;
 }
 
-template <int NPF, bool PRENORM, int MODE, bool PICK>
+template <int NPF, bool PRENORM, int MODE, int PICK>
 static hipError_t rows_t(const float* x, int K, const float* gpre, const float* g,
                          const uint8_t* W, int N, float w_scale, float* out, float* pv, int* pi,
-                         hipStream_t s) {
+                         hipStream_t s, float temp = 1.0f) {
   const size_t lds = lds_bytes(K);
   const dim3 grid(rows_blocks<NPF>(N, K)), block(256);
   if (K % 64 != 0) return hipErrorInvalidValue;
   if (K == 1024)
     hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else if (K == 2048)
     hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else if (K == 4096)
     hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, true>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else if (K <= 1024)
     hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else if (K <= 2048)
     hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else if (K <= 4096)
     hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else if (K <= 8192)
     hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -790,14 +808,14 @@ static hipError_t rows_t(const float* x, int K, const float* gpre, const float* 
 // proj = BitLinear(x) over the per-head in_proj rows
 hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_t* W, int N,
                          float w_scale, float* proj, hipStream_t s) {
-  return rows_t<4, false, 0, false>(x, K, nullptr, gamma, W, N, w_scale, proj, nullptr, nullptr,
+  return rows_t<4, false, 0, 0>(x, K, nullptr, gamma, W, N, w_scale, proj, nullptr, nullptr,
                                     s);
 }
 
 // x += BitLinear(y)  (out_proj with the residual add)
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
                           float w_scale, float* x, hipStream_t s) {
-  return rows_t<2, false, 1, false>(y, K, nullptr, gamma, W, N, w_scale, x, nullptr, nullptr, s);
+  return rows_t<2, false, 1, 0>(y, K, nullptr, gamma, W, N, w_scale, x, nullptr, nullptr, s);
 }
 
 bool inproj_ssm_fits(int K, int hd) { return K % 64 == 0 && K <= 8192 && hd % kCB == 0; }
@@ -849,14 +867,19 @@ hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_b
 // greedy candidates when pick is set
 int lm_head_blocks(int N, int K) { return rows_blocks<16>(N, K); }
 
+// pick: 0 logits only, 1 with the blocks' greedy candidates (part_v,
+// part_i), 2 logits times 1/temp with the blocks' maxima (part_v)
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
-                          const uint8_t* W, int N, float w_scale, float* logits, bool pick,
-                          float* part_v, int* part_i, hipStream_t s) {
-  if (pick)
-    return rows_t<16, true, 0, true>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
-                                     s);
-  return rows_t<16, true, 0, false>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr,
-                                    nullptr, s);
+                          const uint8_t* W, int N, float w_scale, float* logits, int pick,
+                          float temp, float* part_v, int* part_i, hipStream_t s) {
+  if (pick == 1)
+    return rows_t<16, true, 0, 1>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
+                                  s);
+  if (pick == 2)
+    return rows_t<16, true, 0, 2>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, nullptr,
+                                  s, temp);
+  return rows_t<16, true, 0, 0>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr, nullptr,
+                                s);
 }
 
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,

@@ -193,14 +193,15 @@ hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_b
                             float* ssm, const float* D, float* y, const int* ctl, hipStream_t s);
 int lm_head_blocks(int N, int K);
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
-                          const uint8_t* W, int N, float w_scale, float* logits, bool pick,
-                          float* part_v, int* part_i, hipStream_t s);
+                          const uint8_t* W, int N, float w_scale, float* logits, int pick,
+                          float temp, float* part_v, int* part_i, hipStream_t s);
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,
                        int* out_tokens, const float* embed, int dm, float* x, hipStream_t s);
 size_t sample_scratch_bytes(int V);
 hipError_t launch_sample(float* logits, int V, float temp, float min_p, float top_p, int top_k,
-                         uint64_t* rng_state, void* scratch, int* ctl, int* hist, int* out_tokens,
-                         hipStream_t s);
+                         uint64_t* rng_state, void* scratch, const float* pmax, int npart,
+                         int* ctl, int* hist, int* out_tokens, const float* embed, int dm,
+                         float* x, hipStream_t s);
 
 }  // namespace bm
 
@@ -315,8 +316,12 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
   }
   const bool sampled = !(m->temp < 0.05f);  // src/model.c:143-144
   const bool fused_pick = penalty == 1.0f && !sampled;  // x / 1.0f == x * 1.0f == x
+  // sampled without a penalty: the LM head scales by 1/temp itself and
+  // hands its blocks' maxima to the sampler
+  const bool fused_scale = penalty == 1.0f && sampled;
   MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab, m->lm_scale,
-                            m->logits, fused_pick, m->part_v, m->part_i, s));
+                            m->logits, fused_pick ? 1 : (fused_scale ? 2 : 0), m->temp,
+                            m->part_v, m->part_i, s));
   int* out = write_out ? m->out_tokens : nullptr;
   if (sampled) {
     if (penalty != 1.0f) {
@@ -325,10 +330,9 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
       MCHECK(hipGetLastError());
     }
     MCHECK(bm::launch_sample(m->logits, m->vocab, m->temp, m->min_p, m->top_p, m->top_k, m->rng,
-                             m->samp_scratch, m->ctl, m->hist, out, s));
-    hipLaunchKernelGGL(bm::k_embed, dim3((dm + 255) / 256, 1), dim3(256), 0, s, m->embed, dm,
-                       m->vocab, m->ctl + bm::CTL_TOKEN, m->x);
-    MCHECK(hipGetLastError());
+                             m->samp_scratch, fused_scale ? m->part_v : nullptr,
+                             fused_scale ? m->lm_blocks : 0, m->ctl, m->hist, out, m->embed, dm,
+                             m->x, s));
   } else if (fused_pick) {
     MCHECK(bm::launch_pick(m->part_v, m->part_i, m->lm_blocks, m->ctl, m->hist, out, m->embed, dm,
                            m->x, s));
@@ -555,6 +559,8 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
     MCHECK(hipMemcpy(m->rng, &seed0, sizeof(seed0), hipMemcpyHostToDevice));
   }
   MCHECK(hipMalloc(&m->samp_scratch, bm::sample_scratch_bytes(m->vocab)));
+  // the sampler's histogram and block counter start cleared
+  MCHECK(hipMemset(m->samp_scratch, 0, bm::sample_scratch_bytes(m->vocab)));
   MCHECK(hipMalloc(&m->act, bm::act_row_bytes(di > dm ? di : dm)));
   MCHECK(hipMalloc(&m->xq, (size_t)(di > dm ? di : dm)));
   MCHECK(hipDeviceSynchronize());

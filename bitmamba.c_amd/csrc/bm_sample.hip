@@ -1,16 +1,29 @@
 // Device sampler: the reference's sample_advanced (src/model.c:132-361) with
 // filter_and_sample (src/model.c:67-127) and the XorShift64* generator
-// (src/utils.c:117-140), bit for bit, in one 1024-thread block per token.
+// (src/utils.c:117-140), bit for bit.
 //
-// The O(V) passes run on the whole block: temperature scaling and the max
-// logit, the 128-bucket histogram, candidate extraction in ascending index
-// order (a block-wide scan), the exponentials and rescaling, and a stable
-// radix sort where the reference sorts every candidate.  The steps whose
-// result depends on their order stay sequential on one thread, in the
-// reference's order: the heap selections (their array order feeds the
-// sums), every double sum, and the CDF walk.  Sorting is stable like
-// glibc's qsort (a merge sort for these sizes), keyed on the value.
+// The O(V) passes are spread over kFront blocks, each owning a contiguous
+// segment of the vocabulary:
+//   k_samp_scale  temperature scaling in place and the segment's max logit
+//                 (or the LM head does both, with its own blocks' maxima);
+//   k_samp_hist   with the global max, the 128-bucket histogram (global
+//                 atomics of per-block counts) and the segment's
+//                 "pre-candidates" in index order: the logits at or above the
+//                 lowest threshold the extraction can use (the histogram's
+//                 last bucket, or the min_p threshold), a superset of the
+//                 candidates.
+// k_sample then runs the rest on one 1024-thread block: the cutoff bucket,
+// the candidates filtered from the pre-candidate lists in order, selection,
+// softmax, sorting and the draw, the step bookkeeping and the next token's
+// embedding.  (Pass 2 and this in one kernel, with a block counter and
+// device-scope fences handing over to the last block, measured 32 us per
+// token against about 14 for the two launches.)
+// The steps whose result depends on their order stay sequential on one
+// thread, in the reference's order: the heap selections (their array order
+// feeds the sums), every double sum, and the CDF walk.  Sorting is stable
+// like glibc's qsort (a merge sort for these sizes), keyed on the value.
 // Float-to-int bucket indices follow x86 cvttss2si (out of range -> INT_MIN).
+#include "bm_common.h"
 #include "bm_dev.h"
 #include "bm_libm.h"
 
@@ -34,12 +47,54 @@ constexpr int kPartial = 256;      // PARTIAL_K (src/model.c:319)
 constexpr int kStage = 4096;       // candidates staged in LDS per serial pass
 constexpr int kCtlPos = 0, kCtlToken = 1, kCtlStep = 2, kCtlHcount = 3;
 constexpr int kHist = 256;
+constexpr int kFront = 64;          // blocks of the O(V) passes (one wave of partials)
+constexpr int kFrontThreads = 256;
+static_assert(kFront % (kThreads / 64) == 0, "whole pre-candidate lists per wave");
+// vocabularies up to 65535 entries: a segment is at most 4 * kFrontThreads
+static_assert((((65535 + kFront - 1) / kFront + 3) & ~3) <= 4 * kFrontThreads, "one row per block");
+
+// vocabulary segment of each front block: a multiple of 4 entries
+__host__ __device__ __forceinline__ int front_seg(int V) { return ((V + kFront - 1) / kFront + 3) & ~3; }
+
+// scratch: probs[V], pre[kFront * seg] (also the radix sort's second
+// buffer), pmax[kFront], pcnt[kFront], hist[kBuckets].  hist is zero
+// between calls: k_samp_scale clears it, and so does k_sample after use.
+struct Scratch {
+  Cand* probs;
+  Cand* pre;
+  float* pmax;
+  int* pcnt;
+  int* hist;
+};
+__host__ __device__ __forceinline__ Scratch scratch_of(void* base, int V) {
+  Scratch s;
+  s.probs = (Cand*)base;
+  s.pre = s.probs + V;
+  s.pmax = (float*)(s.pre + (size_t)kFront * front_seg(V));
+  s.pcnt = (int*)(s.pmax + kFront);
+  s.hist = s.pcnt + kFront;
+  return s;
+}
+
+// where the token goes: with ctl, the step bookkeeping of k_argmax_step and
+// (with embed) the next token's embedding row into x; without, out_tokens[0]
+struct StepIO {
+  int* ctl;
+  int* hist;
+  int* out_tokens;
+  const float* embed;
+  int dm;
+  float* x;
+};
+
+constexpr int kCandLds = 512;      // candidates kept in LDS when they fit
+constexpr int kListsPerWave = kFront / (kThreads / 64);
 
 struct Smem {
   Cand stage[kStage];
+  Cand cand[kCandLds];
   Cand sel[kPartial];
   Cand sorted[kPartial];
-  int hist[kBuckets];
   unsigned scan[kThreads];
   float fred[kThreads / 64];
   int ired[kThreads / 64];
@@ -63,6 +118,56 @@ __device__ __forceinline__ float rng_float(uint64_t& s) {
 // (int)f as x86-64 cvttss2si computes it
 __device__ __forceinline__ int cvtt_x86(float f) {
   return (f >= -2147483648.0f && f < 2147483648.0f) ? (int)f : (int)0x80000000;
+}
+
+// max of n partial maxima under `x > m` from -1e30f; called by whole waves
+__device__ __forceinline__ float front_max(const float* __restrict__ pmax, int n) {
+  const int lane = threadIdx.x & 63;
+  float v = -1e30f;
+  for (int i = lane; i < n; i += 64) {
+    const float w = pmax[i];
+    if (w > v) v = w;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    if (w > v) v = w;
+  }
+  return __shfl(v, 0, 64);
+}
+
+// min_p threshold before the softmax (src/model.c:168-176)
+__device__ __forceinline__ float min_p_threshold(float max_logit, float min_p) {
+  if (min_p >= 1.0f) return max_logit;
+  if (min_p > 0.0f) return __fadd_rn(max_logit, libm::logf_glibc(min_p));
+  return -1e30f;
+}
+
+__device__ __forceinline__ int effective_k(int top_k) {
+  return (top_k > 0 && top_k <= 256) ? top_k : 0;  // src/model.c:168-170
+}
+
+__device__ __forceinline__ float bucket_scale_of() {
+  return cr_divf((float)(kBuckets - 1), 20.0f);  // src/model.c:182
+}
+
+// extraction threshold for a cutoff bucket (src/model.c:208-213).  It does
+// not increase with the cutoff, so cutoff kBuckets-1 gives the lowest.
+__device__ __forceinline__ float extract_threshold(float max_logit, float min_p_thresh,
+                                                   int cutoff) {
+  const float bucket_thresh =
+      __fsub_rn(max_logit, cr_divf((float)(cutoff + 1), bucket_scale_of()));
+  return bucket_thresh > min_p_thresh ? bucket_thresh : min_p_thresh;
+}
+
+// p[i..i+3] with zeros at and past `end`; p is 16-byte aligned, i % 4 == 0
+__device__ __forceinline__ float4 load4(const float* __restrict__ p, int i, int end) {
+  if (i + 4 <= end) return *(const float4*)(p + i);
+  float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (i < end) r.x = p[i];
+  if (i + 1 < end) r.y = p[i + 1];
+  if (i + 2 < end) r.z = p[i + 2];
+  return r;
 }
 
 __device__ __forceinline__ void heap_sift_down(Cand* h, int n, int i) {
@@ -113,28 +218,59 @@ __device__ unsigned block_scan(unsigned c, Smem& sm, unsigned* total) {
   return incl - c;
 }
 
-// candidates (i, logits[i]) with logits[i] >= thr, ascending i
-__device__ int extract(const float* __restrict__ logits, int V, float thr, Cand* __restrict__ out,
-                       Smem& sm) {
-  const int per = (V + kThreads - 1) / kThreads;
-  const int i0 = threadIdx.x * per, i1 = min(V, i0 + per);
-  unsigned c = 0;
-  for (int i = i0; i < i1; ++i) c += logits[i] >= thr;
-  unsigned total;
-  unsigned o = block_scan(c, sm, &total);
-  for (int i = i0; i < i1; ++i) {
-    const float v = logits[i];
-    if (v >= thr) out[o++] = Cand{i, v};
+// the candidates (i, v) with v >= thr in ascending i, from the front
+// blocks' pre-candidate lists (each in index order, the blocks' segments
+// ascending; pc: this wave's list lengths).  Wave w takes lists
+// kListsPerWave * w .. + kListsPerWave - 1 and writes after the waves before
+// it: into sm.cand when they all fit, else to `spill`.  Returns the count,
+// the array in *out.
+__device__ int gather(const Scratch& sc, const int (&pc)[kListsPerWave], int seg, float thr,
+                      Cand* spill, Cand** out, Smem& sm) {
+  constexpr int NW = kThreads / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < kListsPerWave; ++j) {
+    const Cand* src = sc.pre + (size_t)(wave * kListsPerWave + j) * seg;
+    for (int i = lane; i < pc[j]; i += 64) cnt += src[i].val >= thr;
+  }
+  cnt = wave_sum_i32(cnt);
+  if (lane == 0) sm.ired[wave] = cnt;
+  __syncthreads();
+  int off = 0, total = 0;
+  for (int w = 0; w < NW; ++w) {
+    const int c = sm.ired[w];
+    off += w < wave ? c : 0;
+    total += c;
   }
   __syncthreads();
-  return (int)total;
+  Cand* dst = total <= kCandLds ? sm.cand : spill;
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int j = 0; j < kListsPerWave; ++j) {
+    const Cand* src = sc.pre + (size_t)(wave * kListsPerWave + j) * seg;
+    for (int i0 = 0; i0 < pc[j]; i0 += 64) {
+      const int i = i0 + lane;
+      Cand x{0, 0.0f};
+      if (i < pc[j]) x = src[i];
+      const bool h = i < pc[j] && x.val >= thr;
+      const uint64_t m = __ballot(h);
+      if (h) dst[off + __popcll(m & below)] = x;
+      off += __popcll(m);
+    }
+  }
+  __syncthreads();
+  *out = dst;
+  return total;
 }
 
-// first index of the maximum, starting from index 0 (src/model.c:225-233,
-// 285-291): a later value wins only when strictly greater, so a NaN at index
-// 0 is never beaten and NaNs elsewhere never win.  Returned to every thread.
-__device__ int argmax_from0(const float* __restrict__ logits, int V, Smem& sm) {
-  float bv = logits[0];
+// the sequential scan `best = 0, best_v = init; if (logits[i] > best_v) ...`
+// over i = 0 .. V-1: init = logits[0] in the pruned-everything guards
+// (src/model.c:225-233, 285-291), -1e9f in the greedy branch
+// (src/model.c:144-154).  A later value wins only when strictly greater, so
+// NaNs never win.  Returned to every thread.
+__device__ int argmax_scan(const float* __restrict__ logits, int V, float init, Smem& sm) {
+  float bv = init;
   int bi = 0;
   for (int i = threadIdx.x; i < V; i += kThreads) {
     const float v = logits[i];
@@ -311,8 +447,50 @@ __device__ int filter_and_sample(const Cand* __restrict__ c, int n, float top_p,
   return token;
 }
 
+// the entries of c[0..m) (m <= kStage) whose value is above `root`, in
+// order, into sm.stage; returns their count.  Wave w takes entries
+// 256w .. 256w+255, four per lane.
+__device__ int stage_above(const Cand* __restrict__ c, int m, float root, Smem& sm) {
+  constexpr int NW = kThreads / 64, PER = kStage / NW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  Cand x[PER / 64];
+  uint64_t mk[PER / 64];
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < PER / 64; ++j) {
+    const int i = wave * PER + 64 * j + lane;
+    bool h = false;
+    if (i < m) {
+      x[j] = c[i];
+      h = x[j].val > root;
+    }
+    mk[j] = __ballot(h);
+    cnt += __popcll(mk[j]);
+  }
+  if (lane == 0) sm.ired[wave] = cnt;
+  __syncthreads();
+  int off = 0, total = 0;
+  for (int w = 0; w < NW; ++w) {
+    const int cw = sm.ired[w];
+    off += w < wave ? cw : 0;
+    total += cw;
+  }
+#pragma unroll
+  for (int j = 0; j < PER / 64; ++j) {
+    if ((mk[j] >> lane) & 1ull) sm.stage[off + __popcll(mk[j] & below)] = x[j];
+    off += __popcll(mk[j]);
+  }
+  __syncthreads();
+  return total;
+}
+
 // min-heap selection of the k largest of c[0..n) (src/model.c:238-250,
-// 322-337), one thread; c is global memory, staged through LDS
+// 322-337), one thread; c is global memory, staged through LDS.  The root
+// never decreases (a replacement is larger than the old root, and after the
+// sift the root is the replacement or a child that was not below the old
+// root), so entries not above the root when their chunk is staged would be
+// passed over and are not staged.
 __device__ void heap_select(const Cand* __restrict__ c, int n, int k, Cand* heap, Smem& sm) {
   for (int i = threadIdx.x; i < k; i += kThreads) heap[i] = c[i];
   __syncthreads();
@@ -321,10 +499,9 @@ __device__ void heap_select(const Cand* __restrict__ c, int n, int k, Cand* heap
   for (int c0 = k; c0 < n; c0 += kStage) {
     const int m = min(kStage, n - c0);
     __syncthreads();
-    for (int i = threadIdx.x; i < m; i += kThreads) sm.stage[i] = c[c0 + i];
-    __syncthreads();
+    const int kept = stage_above(c + c0, m, heap[0].val, sm);
     if (threadIdx.x == 0)
-      for (int i = 0; i < m; ++i)
+      for (int i = 0; i < kept; ++i)
         if (sm.stage[i].val > heap[0].val) {
           heap[0] = sm.stage[i];
           heap_sift_down(heap, k, 0);
@@ -348,70 +525,217 @@ __device__ double ordered_sum(const Cand* __restrict__ c, int n, Smem& sm) {
   return s;
 }
 
+// the generator state back, then the step bookkeeping of k_argmax_step
+// (or, without ctl, the token alone); one thread
+__device__ void finish_step(int token, uint64_t rng, uint64_t* rng_state, const StepIO& io) {
+  *rng_state = rng;
+  if (!io.ctl) {
+    io.out_tokens[0] = token;
+    return;
+  }
+  int* ctl = io.ctl;
+  const int step = ctl[kCtlStep];
+  if (io.out_tokens) io.out_tokens[step] = token;
+  ctl[kCtlStep] = step + 1;
+  ctl[kCtlToken] = token;
+  io.hist[ctl[kCtlHcount] % kHist] = token;
+  ctl[kCtlHcount] += 1;
+  ctl[kCtlPos] = ctl[kCtlPos] + 1 < 3 ? ctl[kCtlPos] + 1 : 0;  // src/block.c:107
+}
+
+// the next token's embedding row (src/model.c:1116-1122), whole block
+__device__ void embed_next(int token, const StepIO& io) {
+  if (!io.ctl || !io.embed) return;
+  const float* __restrict__ row = io.embed + (size_t)token * io.dm;
+  for (int i = threadIdx.x; i < io.dm; i += kThreads) io.x[i] = row[i];
+}
+
 }  // namespace
 
-// One sampling step plus the step bookkeeping of k_argmax_step.  `logits`
-// is scaled in place by 1/temp like the reference's.  `probs`/`probs2`:
-// V candidates each of scratch.
-__global__ __launch_bounds__(1024) void k_sample(float* __restrict__ logits, int V,
-                                                 SampleParams p, uint64_t* __restrict__ rng_state,
-                                                 Cand* __restrict__ probs, Cand* __restrict__ probs2,
-                                                 int* __restrict__ ctl, int* __restrict__ hist,
-                                                 int* __restrict__ out_tokens) {
-  __shared__ Smem sm;
-  uint64_t rng = *rng_state;
-  int token = 0;
-
-  // temperature and the max logit (src/model.c:160-166)
-  const float inv_temp = cr_divf(1.0f, p.temp);
+// Front pass 1: logits[i] *= 1/temp over the block's segment and the
+// segment's max under `x > m` from -1e30f (src/model.c:160-166).  Block 0
+// also clears the histogram and the block counter of pass 2.  (The LM head
+// can do this pass itself, with its own blocks' maxima.)
+__global__ __launch_bounds__(kFrontThreads) void k_samp_scale(float* __restrict__ logits, int V,
+                                                              float temp, void* scratch) {
+  __shared__ float red[kFrontThreads / 64];
+  const Scratch sc = scratch_of(scratch, V);
+  const int seg = front_seg(V);
+  const int i0 = min(V, (int)blockIdx.x * seg), i1 = min(V, i0 + seg);
+  if (blockIdx.x == 0 && threadIdx.x < kBuckets) sc.hist[threadIdx.x] = 0;
+  const float inv_temp = cr_divf(1.0f, temp);
   float mx = -1e30f;
-  for (int i = threadIdx.x; i < V; i += kThreads) {
-    const float v = __fmul_rn(logits[i], inv_temp);
-    logits[i] = v;
-    if (v > mx) mx = v;
+  for (int i = i0 + 4 * (int)threadIdx.x; i < i1; i += 4 * kFrontThreads) {
+    const float4 q = load4(logits, i, i1);
+    float v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __fmul_rn(v[e], inv_temp);
+      if (i + e < i1 && v[e] > mx) mx = v[e];
+    }
+    if (i + 4 <= i1) {
+      *(float4*)(logits + i) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + e < i1) logits[i + e] = v[e];
+    }
   }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float w = __shfl_xor(mx, o, 64);
+    if (w > mx) mx = w;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  const float max_logit = block_max(mx, sm);
-  // min_p threshold before the softmax (src/model.c:172-176)
-  float min_p_thresh = -1e30f;
-  if (p.min_p >= 1.0f)
-    min_p_thresh = max_logit;
-  else if (p.min_p > 0.0f)
-    min_p_thresh = __fadd_rn(max_logit, libm::logf_glibc(p.min_p));
-  const int eff_k = (p.top_k > 0 && p.top_k <= 256) ? p.top_k : 0;
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kFrontThreads / 64; ++w)
+      if (red[w] > mx) mx = red[w];
+    sc.pmax[blockIdx.x] = mx;
+  }
+}
 
-  if (eff_k > 0) {
-    // bucket histogram and its cutoff (src/model.c:181-214)
-    for (int b = threadIdx.x; b < kBuckets; b += kThreads) sm.hist[b] = 0;
-    __syncthreads();
-    const float bucket_scale = cr_divf((float)(kBuckets - 1), 20.0f);
-    for (int i = threadIdx.x; i < V; i += kThreads) {
-      const float v = logits[i];
-      if (v >= min_p_thresh) {
-        int b = cvtt_x86(__fmul_rn(__fsub_rn(max_logit, v), bucket_scale));
+// Front pass 2, kFront blocks: with the global max (of the npart partial
+// maxima in pmax), each block adds its segment's counts to the 128-bucket
+// histogram over logits >= the min_p threshold (src/model.c:180-194) and
+// writes its pre-candidates: (i, logits[i]) with logits[i] >= the lowest
+// extraction threshold, in index order, to pre[block * seg ..].
+__global__ __launch_bounds__(kFrontThreads) void k_samp_hist(const float* __restrict__ logits,
+                                                             int V, SampleParams p,
+                                                             void* scratch,
+                                                             const float* __restrict__ pmax,
+                                                             int npart) {
+  constexpr int NW = kFrontThreads / 64;
+  __shared__ int bhist[kBuckets];
+  __shared__ int wcnt[NW];
+  const Scratch sc = scratch_of(scratch, V);
+  const int seg = front_seg(V);
+  const int i0 = min(V, (int)blockIdx.x * seg), i1 = min(V, i0 + seg);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float4 q = load4(logits, i0 + 4 * (int)threadIdx.x, i1);  // before the max: independent
+  const float max_logit = front_max(pmax, npart);
+  const float min_p_thresh = min_p_threshold(max_logit, p.min_p);
+  const int eff_k = effective_k(p.top_k);
+  const bool use_hist = eff_k > 0;
+  const float bucket_scale = bucket_scale_of();
+  const float pre_thresh =
+      use_hist ? extract_threshold(max_logit, min_p_thresh, kBuckets - 1) : min_p_thresh;
+  if (threadIdx.x < kBuckets) bhist[threadIdx.x] = 0;
+  __syncthreads();
+  const uint64_t below = (1ull << lane) - 1ull;
+  Cand* pre = sc.pre + (size_t)blockIdx.x * seg;
+  int last = 0, off = 0;
+  {
+    const int i = i0 + 4 * (int)threadIdx.x;  // a segment is one row of float4s
+    const float v[4] = {q.x, q.y, q.z, q.w};
+    bool h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool in = i + e < i1;
+      if (use_hist && in && v[e] >= min_p_thresh) {
+        int b = cvtt_x86(__fmul_rn(__fsub_rn(max_logit, v[e]), bucket_scale));
         if (b >= kBuckets) b = kBuckets - 1;
         if (b < 0) b = 0;
-        atomicAdd(&sm.hist[b], 1);
+        // the last bucket (20 or more below the max) takes most of the
+        // vocabulary without a min_p threshold: counted in a register
+        if (b == kBuckets - 1)
+          ++last;
+        else
+          atomicAdd(&bhist[b], 1);
       }
+      h[e] = in && v[e] >= pre_thresh;
+    }
+    // order-preserving compaction: lanes in order, then the waves
+    uint64_t m[4];
+    int wn = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      m[e] = __ballot(h[e]);
+      wn += __popcll(m[e]);
+    }
+    if (lane == 0) wcnt[wave] = wn;
+    __syncthreads();
+    int base = off, row = 0;
+    for (int w = 0; w < NW; ++w) {
+      base += w < wave ? wcnt[w] : 0;
+      row += wcnt[w];
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int accum = 0, cutoff = kBuckets - 1;
-      for (int b = 0; b < kBuckets; ++b) {
-        accum += sm.hist[b];
-        if (accum >= eff_k) {
-          cutoff = b;
-          break;
-        }
+    int pos = base;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pos += __popcll(m[e] & below);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (h[e]) pre[pos++] = Cand{i + e, v[e]};
+    off += row;
+  }
+  if (use_hist) {
+    last = wave_sum_i32(last);
+    if (lane == 0 && last) atomicAdd(&bhist[kBuckets - 1], last);
+    __syncthreads();
+    if (threadIdx.x < kBuckets && bhist[threadIdx.x])
+      atomicAdd(&sc.hist[threadIdx.x], bhist[threadIdx.x]);
+  }
+  if (threadIdx.x == 0) sc.pcnt[blockIdx.x] = off;
+}
+
+// The rest of sample_advanced on one 1024-thread block, after the two front
+// passes: the cutoff bucket, the candidates filtered from the pre-candidate
+// lists in order, selection, softmax, sorting and the draw; then the step
+// bookkeeping and the next token's embedding (StepIO).  Leaves the
+// histogram cleared for the next call.
+__global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logits, int V,
+                                                 SampleParams p, uint64_t* __restrict__ rng_state,
+                                                 void* scratch, const float* __restrict__ pmax,
+                                                 int npart, StepIO io) {
+  __shared__ Smem sm;
+  const Scratch sc = scratch_of(scratch, V);
+  const int seg = front_seg(V);
+  // every load that does not depend on another goes out first
+  const int wave = threadIdx.x >> 6;
+  int hc0 = 0, hc1 = 0;
+  if (threadIdx.x < 64) {
+    hc0 = sc.hist[2 * threadIdx.x];
+    hc1 = sc.hist[2 * threadIdx.x + 1];
+  }
+  int pc[kListsPerWave];
+#pragma unroll
+  for (int j = 0; j < kListsPerWave; ++j) pc[j] = sc.pcnt[wave * kListsPerWave + j];
+  uint64_t rng = *rng_state;
+  const float max_logit = front_max(pmax, npart);
+  const float min_p_thresh = min_p_threshold(max_logit, p.min_p);
+  const int eff_k = effective_k(p.top_k);
+  int token = 0;
+  Cand* probs = sc.probs;
+  Cand* probs2 = sc.pre;  // free once the candidates are gathered
+  if (eff_k > 0) {
+    // the cutoff bucket (src/model.c:196-213): first bucket whose running
+    // count reaches k; lane l of wave 0 holds buckets 2l, 2l+1
+    if (threadIdx.x < 64) {
+      const int l = threadIdx.x;
+      const int c0 = hc0, c1 = hc1;
+      int run = c0 + c1;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int up = __shfl_up(run, o, 64);
+        if (l >= o) run += up;
       }
-      const float bucket_thresh = __fsub_rn(max_logit, cr_divf((float)(cutoff + 1), bucket_scale));
-      sm.fwork[0] = bucket_thresh > min_p_thresh ? bucket_thresh : min_p_thresh;
+      const int before = run - (c0 + c1);
+      const bool at0 = before + c0 >= eff_k, at1 = !at0 && run >= eff_k;
+      const uint64_t hit = __ballot(at0 || at1);
+      int cutoff = kBuckets - 1;
+      if (hit) {
+        const int first = __ffsll((unsigned long long)hit) - 1;
+        const int a0 = __shfl(at0 ? 1 : 0, first, 64);
+        cutoff = 2 * first + (a0 ? 0 : 1);
+      }
+      if (l == 0) sm.fwork[0] = extract_threshold(max_logit, min_p_thresh, cutoff);
     }
     __syncthreads();
     const float extract_thresh = sm.fwork[0];
-    int n = extract(logits, V, extract_thresh, probs, sm);
+    int n = gather(sc, pc, seg, extract_thresh, sc.probs, &probs, sm);
     if (n == 0) {
-      token = argmax_from0(logits, V, sm);
+      token = argmax_scan(logits, V, logits[0], sm);
     } else {
       // top-k by a min-heap when there are more candidates (src/model.c:236-251)
       if (n > eff_k) {
@@ -446,9 +770,9 @@ __global__ __launch_bounds__(1024) void k_sample(float* __restrict__ logits, int
     }
   } else {
     // no top-k: every candidate over the min_p threshold (src/model.c:278-300)
-    int n = extract(logits, V, min_p_thresh, probs, sm);
+    int n = gather(sc, pc, seg, min_p_thresh, sc.probs, &probs, sm);
     if (n == 0) {
-      token = argmax_from0(logits, V, sm);
+      token = argmax_scan(logits, V, logits[0], sm);
     } else {
       for (int i = threadIdx.x; i < n; i += kThreads)
         probs[i].val = libm::expf_glibc(__fsub_rn(probs[i].val, max_logit));
@@ -497,29 +821,79 @@ __global__ __launch_bounds__(1024) void k_sample(float* __restrict__ logits, int
     }
   }
 
-  if (threadIdx.x == 0) {
-    *rng_state = rng;
-    const int step = ctl[kCtlStep];
-    if (out_tokens) out_tokens[step] = token;
-    ctl[kCtlStep] = step + 1;
-    ctl[kCtlToken] = token;
-    hist[ctl[kCtlHcount] % kHist] = token;
-    ctl[kCtlHcount] += 1;
-    ctl[kCtlPos] = ctl[kCtlPos] + 1 < 3 ? ctl[kCtlPos] + 1 : 0;  // src/block.c:107
-  }
+  // the token to every thread, the step, the next embedding; leave the
+  // histogram cleared for the next call
+  if (threadIdx.x == 0) sm.iwork[4] = token;
+  __syncthreads();
+  token = sm.iwork[4];
+  if (threadIdx.x == 0) finish_step(token, rng, rng_state, io);
+  embed_next(token, io);
+  if (threadIdx.x < kBuckets) sc.hist[threadIdx.x] = 0;
 }
 
-size_t sample_scratch_bytes(int V) { return 2 * (size_t)V * sizeof(Cand); }
+// greedy (src/model.c:143-154): logits untouched, the generator state kept
+__global__ __launch_bounds__(1024) void k_sample_greedy(const float* __restrict__ logits, int V,
+                                                        uint64_t* __restrict__ rng_state,
+                                                        StepIO io) {
+  __shared__ Smem sm;
+  const int token = argmax_scan(logits, V, -1e9f, sm);
+  if (threadIdx.x == 0) finish_step(token, *rng_state, rng_state, io);
+  embed_next(token, io);
+}
 
+size_t sample_scratch_bytes(int V) {
+  if (V < 1) return 0;
+  return ((size_t)V + (size_t)kFront * front_seg(V)) * sizeof(Cand) +
+         (2 * kFront + kBuckets) * sizeof(int);
+}
+
+// pmax/npart: the maxima of logits already scaled by 1/temp (the LM head's
+// scaled mode), or nullptr to scale here.  With ctl, the step bookkeeping
+// and, with embed, the next embedding row into x[dm]; without, the token to
+// out_tokens[0].
 hipError_t launch_sample(float* logits, int V, float temp, float min_p, float top_p, int top_k,
-                         uint64_t* rng_state, void* scratch, int* ctl, int* hist, int* out_tokens,
-                         hipStream_t s) {
+                         uint64_t* rng_state, void* scratch, const float* pmax, int npart,
+                         int* ctl, int* hist, int* out_tokens, const float* embed, int dm,
+                         float* x, hipStream_t s) {
   if (V < 1 || V > 65535) return hipErrorInvalidValue;  // 16-bit radix offsets
-  Cand* probs = (Cand*)scratch;
+  if ((uintptr_t)logits % 16) return hipErrorInvalidValue;  // float4 passes
   const SampleParams p{temp, min_p, top_p, top_k};
-  hipLaunchKernelGGL(k_sample, dim3(1), dim3(kThreads), 0, s, logits, V, p, rng_state, probs,
-                     probs + V, ctl, hist, out_tokens);
+  const StepIO io{ctl, hist, out_tokens, embed, dm, x};
+  if (temp < 0.05f) {
+    hipLaunchKernelGGL(k_sample_greedy, dim3(1), dim3(kThreads), 0, s, logits, V, rng_state, io);
+    return hipGetLastError();
+  }
+  if (!pmax) {
+    hipLaunchKernelGGL(k_samp_scale, dim3(kFront), dim3(kFrontThreads), 0, s, logits, V, temp,
+                       scratch);
+    pmax = scratch_of(scratch, V).pmax;
+    npart = kFront;
+  }
+  hipLaunchKernelGGL(k_samp_hist, dim3(kFront), dim3(kFrontThreads), 0, s, logits, V, p, scratch,
+                     pmax, npart);
+  hipLaunchKernelGGL(k_sample, dim3(1), dim3(kThreads), 0, s, logits, V, p, rng_state, scratch,
+                     pmax, npart, io);
   return hipGetLastError();
 }
 
 }  // namespace bm
+
+extern "C" size_t bm_hip_sample_workspace_bytes(int vocab) { return bm::sample_scratch_bytes(vocab); }
+
+extern "C" int bm_hip_sample_advanced(float* logits, int vocab, float temp, float min_p,
+                                      float top_p, int top_k, uint64_t* rng, void* workspace,
+                                      int32_t* token_out, void* stream) {
+  if (!logits || !rng || !workspace || !token_out) {
+    bm_set_error("sample_advanced: null pointer");
+    return -1;
+  }
+  const hipError_t e =
+      bm::launch_sample(logits, vocab, temp, min_p, top_p, top_k, rng, workspace, nullptr, 0,
+                        nullptr, nullptr, token_out, nullptr, 0, nullptr, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    bm_set_error("sample_advanced: %s (vocab %d, logits %p; vocab 1..65535, 16-byte aligned logits)",
+                 hipGetErrorString(e), vocab, (void*)logits);
+    return -1;
+  }
+  return 0;
+}

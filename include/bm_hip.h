@@ -274,6 +274,25 @@ int bm_hip_model_set_sampler(bm_hip_model_t *m,
                              float min_p,
                              float top_p,
                              int top_k);
+/* sample_advanced (src/model.c:132-361) on its own: one token from
+ * logits[vocab] (device memory, 16-byte aligned; scaled in place by 1/temp
+ * as the reference leaves them), advancing the XorShift64* state *rng
+ * (device memory, src/utils.c:117-140); temp < 0.05 is the greedy branch.
+ * workspace: bm_hip_sample_workspace_bytes(vocab) bytes of device memory
+ * (the reference's probs buffer, twice).  The token goes to token_out[0]
+ * (device memory); enqueued on `stream`, no synchronization.  0, or -1 for
+ * vocab outside 1..65535, misaligned logits or a null pointer. */
+size_t bm_hip_sample_workspace_bytes(int vocab);
+int bm_hip_sample_advanced(float *logits,
+                           int vocab,
+                           float temp,
+                           float min_p,
+                           float top_p,
+                           int top_k,
+                           uint64_t *rng,
+                           void *workspace,
+                           int32_t *token_out,
+                           void *stream);
 /* rng_seed (src/utils.c:121-124) for the model's device generator; the
  * model starts with the reference's default state. */
 int bm_hip_model_seed(bm_hip_model_t *m, uint64_t seed);
