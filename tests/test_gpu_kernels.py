@@ -93,6 +93,54 @@ def test_quantize_random_vs_oracle(hip, n):
     same_bits(sc, osc, "sc")
 
 
+def _chain_rows(n, seed):
+    """Rows whose sums of squares stress an exact sequential fp32 sum: ties
+    of the running sum's rounding (1 and 4096 mixed: x^2 = 1 is half an ulp
+    once the sum passes 2^24), powers of two, denormal squares, zeros, an
+    overflow to inf, and outliers in normal data."""
+    r = rnd(seed)
+    rows = [
+        np.where(r.random(n) < 0.02, 4096.0, 1.0),
+        np.ldexp(1.0, r.integers(-20, 20, n)) * r.choice([-1.0, 1.0], n),
+        r.integers(-3, 4, n).astype(np.float64),
+        r.standard_normal(n) * 1e-23,
+        np.zeros(n),
+        np.where(np.arange(n) == n // 3, 3.0, 0.0),
+        np.where(np.arange(n) == n // 2, 1e20, r.standard_normal(n)),
+        r.standard_normal(n) * np.where(r.random(n) < 0.01, 1e4, 1.0),
+        np.where(r.random(n) < 0.5, 2048.0, r.integers(1, 64, n).astype(np.float64)),
+    ]
+    return np.ascontiguousarray(np.stack(rows).astype(np.float32))
+
+
+@pytest.mark.parametrize("n", [1024, 2048, 4096, 8192, 1040, 300])
+def test_quantize_chain_edge_rows(hip, n):
+    """The generic per-token quantizer (a row stride that is not a multiple
+    of 4 selects it at every n) on rows built to break an inexact sum of
+    squares, bit-exact against the oracle."""
+    note("quantize chain edge rows n=%d" % n)
+    x = _chain_rows(n, 40 + n)
+    M = x.shape[0]
+    g = (rnd(n).standard_normal(n) * 0.02).astype(np.float32)
+    xs = np.zeros((M, n + 1), np.float32)
+    xs[:, :n] = x
+    dx, dg = DB.from_array(xs), DB.from_array(g)
+    dn, dq, ds = DB(4 * M * n), DB(M * n), DB(4 * M)
+    bh.check(hip.bm_hip_quantize_dev(dx.ptr, M, n, n + 1, dg.ptr, dn.ptr, dq.ptr, n, ds.ptr,
+                                     None, None), "quantize")
+    hip.bm_hip_synchronize()
+    on, oq, osc, _ = native.orc_quantize_rows(x, g)
+    same_bits(dn.download((M, n), np.float32), on, "xn")
+    np.testing.assert_array_equal(dq.download((M, n), np.int8), oq)
+    same_bits(ds.download(M, np.float32), osc, "sc")
+    for i in range(M):
+        out = np.empty(n, np.float32)
+        hip.hip_rms_norm(ptr(x[i]), n, ptr(g), ptr(out))
+        ref = np.empty(n, np.float32)
+        native.oracle().orc_rms_norm(ptr(np.ascontiguousarray(x[i])), n, ptr(g), ptr(ref))
+        same_bits(out, ref, "rms_norm row %d" % i)
+
+
 def test_rms_norm_dropin(hip):
     r = rnd(3)
     for n in (1024, 2048, 777):

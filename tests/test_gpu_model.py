@@ -106,6 +106,43 @@ def test_tiny_model_logits_and_state(hip, penalty):
         m.free()
 
 
+@pytest.mark.parametrize("d_model,n_heads,penalty", [(1024, 32, 1.0), (2048, 64, 1.3)])
+def test_wide_model_logits_vs_oracle(hip, d_model, n_heads, penalty):
+    """Two-layer models at the 255M and 1B widths (2000-token vocabulary):
+    the prefill state and every step's logits bit-exact against the oracle.
+    At these widths (K = 1024, 2048, 4096) the decode kernels keep their
+    input in registers and run the register-resident sums of squares."""
+    note("wide model d_model=%d penalty=%g" % (d_model, penalty))
+    blob = bh.synth_model(2000, d_model, 2, n_heads, 77 + d_model, bh.SYNTH_UNIFORM)
+    prompt = bh.synth_prompt(77, 2000, 8)
+    m = bh.Model(blob)
+    O, h = _oracle_model(blob)
+    try:
+        p = prompt[:-1].copy()
+        m.prefill(p)
+        O.orc_model_prefill(h, ptr(p), p.size)
+        for layer in range(m.n_layers):
+            cs, ss, pos = m.layer_state(layer)
+            ocs = np.empty((3, m.d_inner), np.float32)
+            oss = np.empty(m.d_inner, np.float32)
+            assert pos == O.orc_model_layer_state(h, layer, ptr(ocs), ptr(oss))
+            same_bits(cs, ocs, "conv_state[%d]" % layer)
+            same_bits(ss, oss, "ssm_state[%d]" % layer)
+        hist, cur = [int(t) for t in prompt], int(prompt[-1])
+        for s in range(6):
+            harr = np.array(hist[-256:], np.int32)
+            a = m.step(cur, harr, penalty)
+            b = O.orc_model_step(h, cur, ptr(harr), harr.size, penalty)
+            same_bits(m.logits(), np.ctypeslib.as_array(O.orc_model_logits(h), (m.vocab,)),
+                      "logits step %d" % s)
+            assert a == b
+            hist.append(a)
+            cur = a
+    finally:
+        O.orc_model_free(h)
+        m.free()
+
+
 def test_tiny_generate_matches_reference(hip):
     g = gold("tiny")
     blob, prompt, steps = model_image(g)
