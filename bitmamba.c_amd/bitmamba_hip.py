@@ -30,6 +30,17 @@ class SynthConfig(C.Structure):
                 ("ternary_scale", _f), ("seed", _u64)]
 
 
+class Bit2Tensor(C.Structure):
+    """bm_bit2_tensor_t (bitmamba.c_amd/host/bm_bit2.h)."""
+    _fields_ = [("data", _fp), ("packed", _u8p), ("rows", _i), ("cols", _i),
+                ("n_elements", _sz), ("is_bitnet", C.c_bool), ("scale", _f)]
+
+
+class Bit2View(C.Structure):
+    _fields_ = [("vocab", _i), ("d_model", _i), ("n_layers", _i), ("n_heads", _i),
+                ("n_tensors", _i), ("tensors", C.POINTER(Bit2Tensor))]
+
+
 class Dispatch(C.Structure):
     """Layout mirror of kernel_dispatch_t (src/dispatch.h:87-95)."""
     _fields_ = [("rms_norm", _vp), ("bitlinear_forward", _vp),
@@ -91,6 +102,8 @@ SIGNATURES = {
     "bm_hip_model_decode": (_i, [_vp, _i, _f, C.POINTER(C.c_double)]),
     "bm_hip_model_tokens": (_i, [_vp, _vp, _i]),
     "bm_hip_libm_eval_dev": (_i, [_i, _vp, _vp, _sz, _vp]),
+    "bm_bit2_parse": (_i, [_vp, _sz, C.POINTER(Bit2View)]),
+    "bm_bit2_view_free": (None, [C.POINTER(Bit2View)]),
     "bm_bit2_synth_size": (_sz, [C.POINTER(SynthConfig)]),
     "bm_bit2_synth_write": (_i, [C.POINTER(SynthConfig), _vp, _sz]),
     "bm_synth_ternary": (None, [_u64, _i, _i, _i, _i, _vp]),
@@ -169,6 +182,21 @@ def synth_model(vocab, d_model, n_layers, n_heads, seed, dist=SYNTH_UNIFORM, fp_
     buf = np.empty(n, dtype=np.uint8)
     check(lib().bm_bit2_synth_write(C.byref(cfg), ptr(buf), n), "bm_bit2_synth_write")
     return buf
+
+
+BM_L_IN_NORM, BM_L_IN_PROJ, BM_L_OUT_NORM, BM_L_OUT_PROJ = 0, 1, 7, 8  # bm_bit2.h
+
+
+def image_tensors(blob, layer, which):
+    """struct tensor views (pointing into blob) of one layer entry of a
+    BIT2 image: the reference's model_load view of the same bytes."""
+    v = Bit2View()
+    check(lib().bm_bit2_parse(ptr(blob), blob.nbytes, C.byref(v)), "bm_bit2_parse")
+    try:
+        t = v.tensors[1 + 9 * layer + which]
+        return Tensor(t.data, t.packed, t.rows, t.cols, t.n_elements, t.is_bitnet, t.scale)
+    finally:
+        lib().bm_bit2_view_free(C.byref(v))
 
 
 # ---------------------------------------------------------------------------

@@ -33,9 +33,14 @@ extern "C" const char* bm_hip_last_error(void) { return g_err; }
 
 namespace {
 
+// calls whose inputs and outputs fit here skip the DMA copies: the kernels
+// read x from, and write their results to, mapped host memory
+constexpr size_t kZeroCopyMax = 256 * 1024;
+
 struct DevBuf {
   void* ptr = nullptr;
   size_t bytes = 0;
+  void* dev = nullptr;  // device address of a mapped host buffer
 };
 
 struct Registered {
@@ -54,9 +59,10 @@ struct Backend {
   std::unordered_map<const void*, Registered> floats;
   // grow-on-demand device scratch for the host-pointer entry points; d_w
   // and d_g receive tensors that belong to no registered image, per call
-  DevBuf d_x, d_out, d_norm, d_q, d_act, d_scale, d_w, d_g;
-  // pinned host staging
-  DevBuf h_stage;
+  DevBuf d_x, d_out, d_act, d_scale, d_w, d_g;
+  // pinned host staging (copies), and mapped coherent host memory that
+  // the kernels of small calls read and write directly
+  DevBuf h_stage, h_zc;
 };
 
 Backend& B() {
@@ -89,6 +95,25 @@ bool ensure_pinned(DevBuf& b, size_t bytes) {
   BM_HIP_CHECK_RET(hipHostMalloc(&b.ptr, want, hipHostMallocDefault), false);
   b.bytes = want;
   return true;
+}
+
+bool ensure_mapped(DevBuf& b, size_t bytes) {
+  if (b.bytes >= bytes && b.ptr) return true;
+  if (b.ptr) (void)hipHostFree(b.ptr);
+  b = DevBuf{};
+  void* p = nullptr;
+  BM_HIP_CHECK_RET(hipHostMalloc(&p, kZeroCopyMax, hipHostMallocMapped | hipHostMallocCoherent),
+                   false);
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess) {
+    (void)hipHostFree(p);
+    bm_set_error("hipHostGetDevicePointer failed");
+    return false;
+  }
+  b.ptr = p;
+  b.dev = d;
+  b.bytes = kZeroCopyMax;
+  return bytes <= kZeroCopyMax;
 }
 
 bool init_locked(Backend& b) {
@@ -197,36 +222,42 @@ void host_bitlinear(const float* x, int M, int n, const uint8_t* packed, int row
   const size_t obytes = (size_t)M * rows * sizeof(float);
   const size_t qbytes = (size_t)M * n;
   const size_t abytes = (size_t)M * bm::act_row_bytes(n);
-  if (!ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_out, obytes) ||
-      !ensure_dev(b.d_norm, xbytes) || !ensure_dev(b.d_q, qbytes) ||
+  // the results leave in one copy: [out | x_norm | int8] at 256-byte
+  // aligned offsets, the same in the device buffer and the pinned stage
+  const size_t o_norm = bm::align_up(obytes, 256), o_q = o_norm + bm::align_up(xbytes, 256);
+  const size_t iobytes = o_q + qbytes;
+  if (!ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_out, iobytes) ||
       !ensure_dev(b.d_act, abytes) || !ensure_dev(b.d_scale, (size_t)M * 4))
     die("scratch allocation");
-  const size_t stage = xbytes > obytes + xbytes + qbytes ? xbytes : obytes + xbytes + qbytes;
-  if (!ensure_pinned(b.h_stage, stage)) die("pinned staging");
+  if (!ensure_pinned(b.h_stage, xbytes > iobytes ? xbytes : iobytes)) die("pinned staging");
 
-  uint8_t* hs = (uint8_t*)b.h_stage.ptr;
-  memcpy(hs, x, xbytes);
+  // small calls: [x | out | x_norm | int8] in mapped host memory, no copies
+  const size_t o_x = bm::align_up(iobytes, 256);
+  const bool zc = o_x + xbytes <= kZeroCopyMax && ensure_mapped(b.h_zc, o_x + xbytes);
+  uint8_t* hs = zc ? (uint8_t*)b.h_zc.ptr : (uint8_t*)b.h_stage.ptr;
+  uint8_t* dio = zc ? (uint8_t*)b.h_zc.dev : (uint8_t*)b.d_out.ptr;
+  const float* dx = zc ? (const float*)(dio + o_x) : (const float*)b.d_x.ptr;
   hipStream_t s = b.stream;
-  hipError_t e = hipMemcpyAsync(b.d_x.ptr, hs, xbytes, hipMemcpyHostToDevice, s);
+  hipError_t e = hipSuccess;
+  if (zc) {
+    memcpy(hs + o_x, x, xbytes);
+  } else {
+    memcpy(hs, x, xbytes);
+    e = hipMemcpyAsync(b.d_x.ptr, hs, xbytes, hipMemcpyHostToDevice, s);
+  }
   const bool generic = bm::product_needs_generic(M, cols);
   if (e == hipSuccess)
-    e = bm::launch_quantize((const float*)b.d_x.ptr, M, n, n, dG, (float*)b.d_norm.ptr,
-                            (int8_t*)b.d_q.ptr, n, (float*)b.d_scale.ptr,
-                            generic ? nullptr : (uint8_t*)b.d_act.ptr, s);
+    e = bm::launch_quantize(dx, M, n, n, dG, (float*)(dio + o_norm), (int8_t*)(dio + o_q), n,
+                            (float*)b.d_scale.ptr, generic ? nullptr : (uint8_t*)b.d_act.ptr, s);
   if (e == hipSuccess) {
     if (generic)
-      e = bm::launch_generic((const int8_t*)b.d_q.ptr, n, (const float*)b.d_scale.ptr, M, dW,
-                             rows, cols, w_scale, b.d_out.ptr, bm::MODE_STORE, s);
+      e = bm::launch_generic((const int8_t*)(dio + o_q), n, (const float*)b.d_scale.ptr, M, dW,
+                             rows, cols, w_scale, dio, bm::MODE_STORE, s);
     else
       e = bm::launch_product((const uint8_t*)b.d_act.ptr, (const float*)b.d_scale.ptr, M, dW,
-                             rows, cols, w_scale, true, b.d_out.ptr, bm::MODE_STORE, s);
+                             rows, cols, w_scale, true, dio, bm::MODE_STORE, s);
   }
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(hs, b.d_out.ptr, obytes, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(hs + obytes, b.d_norm.ptr, xbytes, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(hs + obytes + xbytes, b.d_q.ptr, qbytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && !zc) e = hipMemcpyAsync(hs, dio, iobytes, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     bm_set_error("%s", hipGetErrorString(e));
@@ -235,10 +266,10 @@ void host_bitlinear(const float* x, int M, int n, const uint8_t* packed, int row
   memcpy(out, hs, obytes);
   // x_norm_buf is a single n-vector reused per token: the last token stays
   if (x_norm_buf)
-    memcpy(x_norm_buf, hs + obytes + (size_t)(M - 1) * n * sizeof(float), (size_t)n * 4);
+    memcpy(x_norm_buf, hs + o_norm + (size_t)(M - 1) * n * sizeof(float), (size_t)n * 4);
   if (x_quant)
     for (int m = 0; m < M; ++m)
-      memcpy(x_quant + (size_t)m * quant_stride, hs + obytes + xbytes + (size_t)m * n, (size_t)n);
+      memcpy(x_quant + (size_t)m * quant_stride, hs + o_q + (size_t)m * n, (size_t)n);
 }
 
 }  // namespace
@@ -292,12 +323,14 @@ extern "C" void bm_hip_cleanup(void) {
   for (auto& kv : b.floats) (void)hipFree(kv.second.dev);
   b.packed.clear();
   b.floats.clear();
-  for (DevBuf* d : {&b.d_x, &b.d_out, &b.d_norm, &b.d_q, &b.d_act, &b.d_scale, &b.d_w, &b.d_g}) {
+  for (DevBuf* d : {&b.d_x, &b.d_out, &b.d_act, &b.d_scale, &b.d_w, &b.d_g}) {
     if (d->ptr) (void)hipFree(d->ptr);
     *d = DevBuf{};
   }
-  if (b.h_stage.ptr) (void)hipHostFree(b.h_stage.ptr);
-  b.h_stage = DevBuf{};
+  for (DevBuf* h : {&b.h_stage, &b.h_zc}) {
+    if (h->ptr) (void)hipHostFree(h->ptr);
+    *h = DevBuf{};
+  }
   (void)hipStreamDestroy(b.stream);
   b.stream = nullptr;
   b.ready = false;
@@ -312,18 +345,19 @@ extern "C" float hip_rms_norm(const float* x, int size, const float* weight, flo
   if (!init_locked(b)) die("init");
   const float* dG = floats_for_call(b, weight, (size_t)size);
   const size_t xbytes = (size_t)size * sizeof(float);
-  if (!dG || !ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_norm, xbytes) ||
-      !ensure_dev(b.d_scale, 16) || !ensure_pinned(b.h_stage, xbytes + 16))
+  // out and max|out| leave in one copy: [out | max]
+  if (!dG || !ensure_dev(b.d_x, xbytes) || !ensure_dev(b.d_out, xbytes + 16) ||
+      !ensure_pinned(b.h_stage, xbytes + 16))
     die("rms_norm scratch");
   uint8_t* hs = (uint8_t*)b.h_stage.ptr;
+  uint8_t* dio = (uint8_t*)b.d_out.ptr;
   memcpy(hs, x, xbytes);
   hipStream_t s = b.stream;
   hipError_t e = hipMemcpyAsync(b.d_x.ptr, hs, xbytes, hipMemcpyHostToDevice, s);
   if (e == hipSuccess)
-    e = bm::launch_rms_norm((const float*)b.d_x.ptr, size, dG, (float*)b.d_norm.ptr,
-                            (float*)b.d_scale.ptr, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(hs, b.d_norm.ptr, xbytes, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(hs + xbytes, b.d_scale.ptr, 4, hipMemcpyDeviceToHost, s);
+    e = bm::launch_rms_norm((const float*)b.d_x.ptr, size, dG, (float*)dio,
+                            (float*)(dio + xbytes), s);
+  if (e == hipSuccess) e = hipMemcpyAsync(hs, dio, xbytes + 4, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     bm_set_error("%s", hipGetErrorString(e));
