@@ -520,6 +520,158 @@ __global__ __launch_bounds__(256) void k_gemv_mt(const uint8_t* __restrict__ act
 }
 
 // ---------------------------------------------------------------------------
+// Few-token product on int8 MFMA (2 <= M <= 32, K % 128 == 0): the tokens
+// are the 32 rows of v_mfma_i32_32x32x32_i8's A operand (rows past M are
+// zeros and are not stored), 32 weight rows its B operand.  A block
+// of 8 waves owns GPB groups of 32 weight rows; the WPG waves of a group
+// split its 1024-column slices.  Each wave loads a slice's packed weights
+// and the tokens' permuted int8 (cache-resident: every block reads them)
+// with coalesced loads, regroups them for the MFMA lanes through its own
+// LDS, decodes the weights in registers, and leaves one fp32 term
+// per (slice, token, row) in LDS -- (x.code - sum x) / (scale_x * w_scale),
+// exact int32 before the one rounding -- which the block then folds in slice
+// order (src/kernel.c:255-256, 407-425).  Lane (j, h) covers columns
+// 128t + 64h + 16q .. in step q of each 128-column block t.
+// ---------------------------------------------------------------------------
+constexpr int kSmMaxM = 32, kSmMaxSlices = 16;  // K <= 16384
+
+__host__ __device__ inline int sm_wpg(int n_slices) {  // waves per row group: a power of two
+  return n_slices >= 8 ? 8 : (n_slices >= 4 ? 4 : (n_slices >= 2 ? 2 : 1));
+}
+
+template <bool CANON, int MODE>
+__global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ act,
+                                                    size_t act_stride,
+                                                    const float* __restrict__ scale_x, int M,
+                                                    const uint8_t* __restrict__ W, int N, int K,
+                                                    float w_scale, float* __restrict__ out,
+                                                    int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
+  extern __shared__ __attribute__((aligned(16))) float s_part[];  // [slice][32 tokens][GPB*32 rows]
+  __shared__ int s_sx[kSmMaxM][kSmMaxSlices];
+  __shared__ float s_inv[kSmMaxM];
+  __shared__ __attribute__((aligned(16))) uint8_t s_tA[8][32 * 128];  // per wave: one step of A
+  __shared__ __attribute__((aligned(16))) uint8_t s_tB[8][32 * 128];  // per wave: 4 steps of B
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j32 = lane & 31, h = lane >> 5;
+  const int n_slices = slices_of(K);
+  const int wpg = sm_wpg(n_slices), gpb = 8 / wpg, spw = (n_slices + wpg - 1) / wpg;
+  const int rows_b = 32 * gpb;
+  const size_t wstride = (size_t)(K >> 2);
+  const size_t perm = act_perm_off(K);
+
+  for (int i = tid; i < kSmMaxM * n_slices; i += 512) {
+    const int m = i / n_slices, sl = i % n_slices;
+    s_sx[m][sl] = ((const int*)(act + (size_t)min(m, M - 1) * act_stride))[sl];
+  }
+  if (tid < kSmMaxM) s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[min(tid, M - 1)], w_scale);
+  __syncthreads();
+
+  const int g = wave / wpg;                       // row group in the block
+  const int n0 = (blockIdx.x * gpb + g) * 32;     // its first weight row
+  const int cr = lane >> 3, cc = lane & 7;
+  uint8_t* __restrict__ tA = s_tA[wave];
+  uint8_t* __restrict__ tB = s_tB[wave];
+  // 16-byte chunk c of row r (128-byte rows), XOR-swizzled by r % 8 so that
+  // 16 rows read at one chunk index hit distinct banks
+  auto swz = [](int r, int c) __attribute__((always_inline)) { return r * 128 + 16 * (c ^ (r & 7)); };
+  auto wave_lds_sync = []() __attribute__((always_inline)) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  const int sl0 = (wave % wpg) * spw, sl1 = min(n_slices, sl0 + spw);
+  for (int sl = sl0; sl < sl1; ++sl) {
+    const int kb0 = sl * kSlice, kb1 = min(K, kb0 + kSlice);
+    v16i acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0;
+    // The whole slice's operands are requested before the first MFMA, in a
+    // coalesced order (lane l: row l/8 + 8i, 16-byte chunk l%8 of a 128-byte
+    // run), then moved to the MFMA lanes through the wave's own LDS.
+    const int nst = (kb1 - kb0) >> 7;  // 128-column blocks, <= 8
+    const int wb = (kb1 - kb0) >> 2;   // packed bytes of the slice per row
+    v4i ca[kSlice / 128][4], cb[kSlice / 512][4];
+#pragma unroll
+    for (int t = 0; t < kSlice / 128; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = cr + 8 * i;
+        ca[t][i] = (t < nst && m < M)
+                       ? *(const v4i*)(act + (size_t)m * act_stride + perm + kb0 + 128 * t + 16 * cc)
+                       : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+    for (int u = 0; u < kSlice / 512; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(n0 + cr + 8 * i, N - 1);
+        const int off = 128 * u + 16 * cc;
+        cb[u][i] = off < wb ? *(const v4i*)(W + (size_t)r * wstride + (kb0 >> 2) + off)
+                            : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+    for (int t = 0; t < kSlice / 128; ++t) {
+      if (t < nst) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          *(v4i*)(tA + swz(cr + 8 * i, cc)) = ca[t][i];
+          if (t % 4 == 0) *(v4i*)(tB + swz(cr + 8 * i, cc)) = cb[t / 4][i];
+        }
+        wave_lds_sync();
+        const uint4 bw = *(const uint4*)(tB + swz(j32, 2 * (t % 4) + h));
+        v4i ao[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ao[q] = *(const v4i*)(tA + swz(j32, 4 * h + q));
+        wave_lds_sync();  // the reads are done before the next step's writes
+        const uint32_t w4[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t pw = CANON ? w4[q] : canon_codes(w4[q]);
+          v4i bo;
+          bo[0] = (int)(pw & 0x03030303u);
+          bo[1] = (int)((pw >> 2) & 0x03030303u);
+          bo[2] = (int)((pw >> 4) & 0x03030303u);
+          bo[3] = (int)((pw >> 6) & 0x03030303u);
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao[q], bo, acc, 0, 0, 0);
+        }
+      }
+    }
+    // acc element v: token 8(v/4) + 4h + v%4, weight row j32
+    float* __restrict__ part = s_part + (size_t)sl * kSmMaxM * rows_b;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+      const int t = acc[v] - s_sx[m][sl];
+      part[m * rows_b + g * 32 + j32] =
+          I32 ? __int_as_float(t) : __fmul_rn((float)t, s_inv[m]);
+    }
+  }
+  __syncthreads();
+  // fold the slices in order: thread -> (token, row) pairs
+  for (int i = tid; i < M * rows_b; i += 512) {
+    const int m = i / rows_b, r = i % rows_b;
+    const int row = blockIdx.x * rows_b + r;
+    if (row >= N) continue;
+    float o = 0.0f;
+    int tot = 0;
+    for (int sl = 0; sl < n_slices; ++sl) {
+      const float f = s_part[((size_t)sl * kSmMaxM + m) * rows_b + r];
+      if (I32)
+        tot += __float_as_int(f);
+      else
+        o = __fadd_rn(o, f);
+    }
+    const size_t at = (size_t)m * N + row;
+    if (I32)
+      out_i32[at] = tot;
+    else
+      out[at] = MODE == 1 ? __fadd_rn(out[at], o) : o;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic product for any K (K % 64 != 0 or very long rows): one wave per
 // row, plain int8 activations, 1024-column slices then the K % 4 remainder.
 // ---------------------------------------------------------------------------
@@ -915,6 +1067,15 @@ static hipError_t gemv_mt_t(const uint8_t* act, const float* scale_x, int M, con
 template <bool CANON, int MODE>
 static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
                                 int N, int K, float w_scale, void* out, hipStream_t s) {
+  if (M >= 2 && M <= kSmMaxM && K % 128 == 0 && K <= 16384) {
+    const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
+    const dim3 grid((N + 32 * gpb - 1) / (32 * gpb));
+    const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
+    hipLaunchKernelGGL((k_gemm_small<CANON, MODE>), grid, dim3(512), lds, s, act,
+                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                       (int32_t*)out);
+    return hipGetLastError();
+  }
   if (M >= 2 && M <= kMtMaxM && K <= kMtMaxK) {
     if (K <= 1024) return gemv_mt_t<16, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
     if (K <= 2048) return gemv_mt_t<32, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);

@@ -227,7 +227,10 @@ def test_stress_m4096_sampled_and_linear(hip):
 # ------------------------------------------------------------ fp32 BitLinear
 FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257),
              (3, 1024, 300), (1, 1000, 77), (2, 1026, 33), (1, 100, 10),
-             (48, 2048, 520), (40, 4096, 260)]
+             (48, 2048, 520), (40, 4096, 260),
+             # few tokens on MFMA: 1, 2, 3, 4, 5 and 16 slices of 1024 columns
+             (7, 2048, 8512), (16, 4096, 2048), (12, 3072, 100), (9, 5120, 64), (31, 1024, 70),
+             (30, 16384, 40)]
 
 
 @pytest.mark.parametrize("M,K,N", FP_SHAPES)
