@@ -865,7 +865,8 @@ hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_b
 
 // LM head: logits = BitLinear(RMSNorm(x; norm_f); lm_head), plus per-block
 // greedy candidates when pick is set
-int lm_head_blocks(int N, int K) { return rows_blocks<16>(N, K); }
+constexpr int kLmNpf = 16;  // row groups per wave in the LM head
+int lm_head_blocks(int N, int K) { return rows_blocks<kLmNpf>(N, K); }
 
 // pick: 0 logits only, 1 with the blocks' greedy candidates (part_v,
 // part_i), 2 logits times 1/temp with the blocks' maxima (part_v)
@@ -873,12 +874,12 @@ hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const floa
                           const uint8_t* W, int N, float w_scale, float* logits, int pick,
                           float temp, float* part_v, int* part_i, hipStream_t s) {
   if (pick == 1)
-    return rows_t<16, true, 0, 1>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
+    return rows_t<kLmNpf, true, 0, 1>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
                                   s);
   if (pick == 2)
-    return rows_t<16, true, 0, 2>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, nullptr,
+    return rows_t<kLmNpf, true, 0, 2>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, nullptr,
                                   s, temp);
-  return rows_t<16, true, 0, 0>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr, nullptr,
+  return rows_t<kLmNpf, true, 0, 0>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr, nullptr,
                                 s);
 }
 

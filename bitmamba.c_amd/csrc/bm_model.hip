@@ -41,53 +41,119 @@ __device__ __forceinline__ float softplus_ref(float x) {
   return libm::logf_glibc(__fadd_rn(1.0f, libm::expf_glibc(x)));
 }
 
-// One channel of scalar_ssm_inner (src/kernel.c:34-70) for one token.  proj
-// holds the in_proj outputs in the device's per-head order: head h occupies
-// [h*(2hd+3), (h+1)*(2hd+3)) as [z (hd) | x (hd) | B | C | dt].
-__device__ __forceinline__ void ssm_channel(const float* __restrict__ proj, int di, int nh, int hd,
-                                            int idx, int pos, const float* __restrict__ dt_bias,
-                                            const float* __restrict__ A,
-                                            const float* __restrict__ cw,
-                                            const float* __restrict__ cb,
-                                            float* __restrict__ cs, float* __restrict__ ssm,
-                                            const float* __restrict__ D, float* __restrict__ y) {
+// Prefill SSM (ssm_batch_worker, src/block.c:127-160) in three phases.  Of
+// scalar_ssm_inner's per-token work (src/kernel.c:34-70) only the state
+// update st = st * decay + xa * (B * dt) and y = (st * C + xa * D) * silu(z)
+// depend on the previous token; dt, decay, the depthwise conv over the
+// token's three predecessors, silu and the products with B * dt and D do
+// not.  Phase 1 computes those for a chunk of tokens with one thread per
+// (token, channel); phase 2 runs the recurrence, one thread per channel;
+// phase 3 forms y from each token's state, again in parallel.
+// Every value is the same fp32 expression, in the same order, as in the
+// token-serial loop, so the results are bit for bit those of that loop.
+// proj holds the in_proj outputs in the device's per-head order: head h
+// occupies [h*(2hd+3), (h+1)*(2hd+3)) of a token's row as
+// [z (hd) | x (hd) | B | C | dt].
+constexpr int kSsmChunk = 256;  // tokens per phase-1 pass
+enum { PRE_DECAY = 0, PRE_XBDT, PRE_C, PRE_XAD, PRE_SZ, PRE_COUNT };
+
+__global__ void k_ssm_prep(const float* __restrict__ proj, int pd, int t0, int nt, int di, int nh,
+                           int hd, const float* __restrict__ dt_bias, const float* __restrict__ A,
+                           const float* __restrict__ cw, const float* __restrict__ cb,
+                           const float* __restrict__ cs, const float* __restrict__ D,
+                           const int* __restrict__ ctl, float* __restrict__ pre) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (idx >= di || t >= nt) return;
+  const int tg = t0 + t;
   const int h = idx / hd, c = idx - h * hd;
-  const float* __restrict__ ph = proj + (size_t)h * (2 * hd + 3);
-  const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
-  const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
+  const size_t hoff = (size_t)h * (2 * hd + 3);
+  const float* __restrict__ ph = proj + (size_t)tg * pd + hoff;
+  const int pos0 = ctl[CTL_POS];
+  // input of token tg - k: from the batch, or from the conv ring for the
+  // three tokens before it (x_{-j} sits at ring position pos0 + 3 - j)
+  auto prev = [&](int k) {
+    const int tp = tg - k;
+    return tp >= 0 ? proj[(size_t)tp * pd + hoff + hd + c]
+                   : cs[(size_t)((pos0 + 3 + tp) % 3) * di + idx];
+  };
   const float dt_val = softplus_ref(__fadd_rn(ph[2 * hd + 2], dt_bias[h]));
   const float decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
   const float Bdt = __fmul_rn(ph[2 * hd], dt_val);
-  const float C_val = ph[2 * hd + 1];
   const float xin = ph[hd + c];
-  float* c0 = cs + (size_t)pos * di;
-  float conv = __fadd_rn(cb[idx], __fmul_rn(c0[idx], cw[idx]));
-  conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t1 * di + idx], cw[di + idx]));
-  conv = __fadd_rn(conv, __fmul_rn(cs[(size_t)t2 * di + idx], cw[2 * di + idx]));
+  float conv = __fadd_rn(cb[idx], __fmul_rn(prev(3), cw[idx]));
+  conv = __fadd_rn(conv, __fmul_rn(prev(2), cw[di + idx]));
+  conv = __fadd_rn(conv, __fmul_rn(prev(1), cw[2 * di + idx]));
   conv = __fadd_rn(conv, __fmul_rn(xin, cw[3 * di + idx]));
-  c0[idx] = xin;  // the oldest tap is overwritten (cs_write == cs0)
   const float xa = silu_ref(conv);
-  const float st = __fadd_rn(__fmul_rn(ssm[idx], decay), __fmul_rn(xa, Bdt));
-  ssm[idx] = st;
-  y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xa, D[idx])), silu_ref(ph[c]));
+  const size_t plane = (size_t)nt * di, at = (size_t)t * di + idx;
+  pre[PRE_DECAY * plane + at] = decay;
+  pre[PRE_XBDT * plane + at] = __fmul_rn(xa, Bdt);
+  pre[PRE_C * plane + at] = ph[2 * hd + 1];
+  pre[PRE_XAD * plane + at] = __fmul_rn(xa, D[idx]);
+  pre[PRE_SZ * plane + at] = silu_ref(ph[c]);
 }
 
-// n tokens in order; each thread owns one channel across all tokens
-// (ssm_batch_worker, src/block.c:127-160)
-__global__ void k_ssm_batch(const float* __restrict__ proj, int pd, int n, int di, int nh, int hd,
-                            const float* __restrict__ dt_bias, const float* __restrict__ A,
-                            const float* __restrict__ cw, const float* __restrict__ cb,
-                            float* __restrict__ cs, float* __restrict__ ssm,
-                            const float* __restrict__ D, float* __restrict__ y,
-                            const int* __restrict__ ctl) {
+// Phase 2 for tokens t0 .. t0+nt-1: the state recurrence alone, one thread
+// per channel, reading decay and xa * B * dt 32 tokens ahead; each token's
+// state goes to y, which phase 3 turns into the output.  The last chunk
+// (n_total > 0) also leaves the conv ring as the token loop would: the
+// inputs of the last three tokens at their ring positions.
+__global__ __launch_bounds__(64) void k_ssm_scan(const float* __restrict__ pre, int t0, int nt,
+                                                 int di, float* __restrict__ ssm,
+                                                 float* __restrict__ y,
+                                                 const float* __restrict__ proj, int pd, int hd,
+                                                 float* __restrict__ cs,
+                                                 const int* __restrict__ ctl, int n_total) {
+  constexpr int B = 32;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= di) return;
-  int pos = ctl[CTL_POS];
-  for (int t = 0; t < n; ++t) {
-    ssm_channel(proj + (size_t)t * pd, di, nh, hd, idx, pos, dt_bias, A, cw, cb, cs, ssm, D,
-                y + (size_t)t * di);
-    pos = pos + 1 < 3 ? pos + 1 : 0;
+  const size_t plane = (size_t)nt * di;
+  float st = ssm[idx];
+  float dec[2][B], xb[2][B];
+  auto fetch = [&](int buf, int tb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const bool in = tb + j < nt;
+      const size_t at = (size_t)(tb + j) * di + idx;
+      dec[buf][j] = in ? pre[PRE_DECAY * plane + at] : 0.0f;
+      xb[buf][j] = in ? pre[PRE_XBDT * plane + at] : 0.0f;
+    }
+  };
+  auto run = [&](int buf, int tb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (tb + j < nt) {
+        st = __fadd_rn(__fmul_rn(st, dec[buf][j]), xb[buf][j]);
+        y[(size_t)(t0 + tb + j) * di + idx] = st;
+      }
+  };
+  fetch(0, 0);
+  for (int tb = 0; tb < nt; tb += 2 * B) {
+    fetch(1, tb + B);  // past nt: zeros, not used
+    run(0, tb);
+    fetch(0, tb + 2 * B);
+    run(1, tb + B);
   }
+  ssm[idx] = st;
+  if (n_total > 0) {
+    const int h = idx / hd, c = idx - h * hd;
+    const int pos0 = ctl[CTL_POS];
+    for (int k = max(0, n_total - 3); k < n_total; ++k)
+      cs[(size_t)((pos0 + k) % 3) * di + idx] =
+          proj[(size_t)k * pd + (size_t)h * (2 * hd + 3) + hd + c];
+  }
+}
+
+// Phase 3: y = (st * C + xa * D) * silu(z) for every (token, channel) of
+// the chunk, st being the state phase 2 left in y
+__global__ void k_ssm_out(const float* __restrict__ pre, int t0, int nt, int di,
+                          float* __restrict__ y) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (idx >= di || t >= nt) return;
+  const size_t plane = (size_t)nt * di, at = (size_t)t * di + idx;
+  float* __restrict__ yp = y + (size_t)(t0 + t) * di + idx;
+  *yp = __fmul_rn(__fadd_rn(__fmul_rn(*yp, pre[PRE_C * plane + at]), pre[PRE_XAD * plane + at]),
+                  pre[PRE_SZ * plane + at]);
 }
 
 __global__ void k_advance_pos(int* ctl, int n) {
@@ -242,6 +308,7 @@ struct bm_hip_model {
   int8_t* xq = nullptr;
   // prefill scratch (grow on demand)
   float *px = nullptr, *pproj = nullptr, *py = nullptr, *pscale = nullptr;
+  float* ppre = nullptr;  // prefill SSM phase-1 values, PRE_COUNT planes of a chunk
   uint8_t* pact = nullptr;
   int8_t* pxq = nullptr;
   int* ptok = nullptr;
@@ -388,7 +455,7 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
 int ensure_prefill(bm_hip_model* m, int n) {
   if (n <= m->pcap) return 0;
   for (void* p : {(void*)m->px, (void*)m->pproj, (void*)m->py, (void*)m->pscale,
-                  (void*)m->pact, (void*)m->pxq, (void*)m->ptok})
+                  (void*)m->pact, (void*)m->pxq, (void*)m->ptok, (void*)m->ppre})
     if (p) (void)hipFree(p);
   const size_t K = (size_t)(m->di > m->dm ? m->di : m->dm);
   MCHECK(hipMalloc(&m->px, (size_t)n * m->dm * 4));
@@ -398,6 +465,8 @@ int ensure_prefill(bm_hip_model* m, int n) {
   MCHECK(hipMalloc(&m->pact, (size_t)n * bm::act_row_bytes((int)K)));
   MCHECK(hipMalloc(&m->pxq, (size_t)n * K));
   MCHECK(hipMalloc(&m->ptok, (size_t)n * 4));
+  MCHECK(hipMalloc(&m->ppre, (size_t)bm::PRE_COUNT * (n < bm::kSsmChunk ? n : bm::kSsmChunk) *
+                                 m->di * 4));
   m->pcap = n;
   return 0;
 }
@@ -412,7 +481,8 @@ void model_release(bm_hip_model* m) {
                   (void*)m->y, (void*)m->feat, (void*)m->logits, (void*)m->scale,
                   (void*)m->part_v, (void*)m->part_i, (void*)m->rng, m->samp_scratch,
                   (void*)m->act, (void*)m->xq, (void*)m->px, (void*)m->pproj, (void*)m->py,
-                  (void*)m->pscale, (void*)m->pact, (void*)m->pxq, (void*)m->ptok})
+                  (void*)m->pscale, (void*)m->pact, (void*)m->pxq, (void*)m->ptok,
+                  (void*)m->ppre})
     if (p) (void)hipFree(p);
   if (m->ev0) (void)hipEventDestroy(m->ev0);
   if (m->ev1) (void)hipEventDestroy(m->ev1);
@@ -671,16 +741,27 @@ extern "C" int bm_hip_model_prefill(bm_hip_model_t* m, const int32_t* tokens, in
   MCHECK(hipGetLastError());
   for (int l = 0; l < m->nl; ++l) {
     const Layer& Ly = m->L[l];
-    // block_step_batch (src/block.c:378-447): batched in_proj, token-serial
-    // SSM, batched out_proj, then x += out (src/model.c:1139-1142)
+    // block_step_batch (src/block.c:378-447): batched in_proj, the SSM in
+    // three phases per chunk of tokens (k_ssm_prep, k_ssm_scan, k_ssm_out),
+    // batched out_proj, then x += out (src/model.c:1139-1142)
     if (bitlinear(m, m->px, n, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->pproj,
                   bm::MODE_STORE, m->pact, m->pscale, m->pxq, s))
       return -1;
-    hipLaunchKernelGGL(bm::k_ssm_batch, dim3((di + 255) / 256), dim3(256), 0, s, m->pproj, m->pd,
-                       n, di, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b,
-                       m->conv_state + (size_t)l * 3 * di, m->ssm_state + (size_t)l * di, Ly.D,
-                       m->py, m->ctl);
-    MCHECK(hipGetLastError());
+    float* cs = m->conv_state + (size_t)l * 3 * di;
+    for (int t0 = 0; t0 < n; t0 += bm::kSsmChunk) {
+      const int nt = n - t0 < bm::kSsmChunk ? n - t0 : bm::kSsmChunk;
+      hipLaunchKernelGGL(bm::k_ssm_prep, dim3((di + 255) / 256, nt), dim3(256), 0, s, m->pproj,
+                         m->pd, t0, nt, di, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt,
+                         Ly.conv_b, cs, Ly.D, m->ctl, m->ppre);
+      MCHECK(hipGetLastError());
+      hipLaunchKernelGGL(bm::k_ssm_scan, dim3((di + 63) / 64), dim3(64), 0, s, m->ppre, t0, nt,
+                         di, m->ssm_state + (size_t)l * di, m->py, m->pproj, m->pd, m->hd, cs,
+                         m->ctl, t0 + nt == n ? n : 0);
+      MCHECK(hipGetLastError());
+      hipLaunchKernelGGL(bm::k_ssm_out, dim3((di + 255) / 256, nt), dim3(256), 0, s, m->ppre, t0,
+                         nt, di, m->py);
+      MCHECK(hipGetLastError());
+    }
     if (bitlinear(m, m->py, n, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->px,
                   bm::MODE_ACC, m->pact, m->pscale, m->pxq, s))
       return -1;

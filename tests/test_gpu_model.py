@@ -143,6 +143,47 @@ def test_wide_model_logits_vs_oracle(hip, d_model, n_heads, penalty):
         m.free()
 
 
+def test_prefill_lengths_vs_oracle(hip):
+    """Prefill in one call and in several (the conv ring and the state carry
+    over), with 1 to 600 tokens (several 256-token chunks of the two-phase
+    SSM): every layer's state and the next step's logits bit-exact against
+    the oracle's token-serial prefill."""
+    g = gold("tiny")
+    blob, _, _ = model_image(g)
+    c = g["config"]
+    m = bh.Model(blob)
+    O, h = _oracle_model(blob)
+    try:
+        for parts in ([1], [2], [3], [5], [300], [600], [100, 200], [1, 2, 257]):
+            note("prefill parts %s" % parts)
+            m.reset()
+            O.orc_model_free(h)
+            h = O.orc_model_load(ptr(blob), blob.nbytes)
+            toks = bh.synth_prompt(sum(parts) + 11, c["vocab"], sum(parts) + 1)
+            at = 0
+            for n in parts:
+                p = toks[at:at + n].copy()
+                m.prefill(p)
+                O.orc_model_prefill(h, ptr(p), p.size)
+                at += n
+            for layer in range(m.n_layers):
+                cs, ss, pos = m.layer_state(layer)
+                ocs = np.empty((3, m.d_inner), np.float32)
+                oss = np.empty(m.d_inner, np.float32)
+                assert pos == O.orc_model_layer_state(h, layer, ptr(ocs), ptr(oss))
+                same_bits(cs, ocs, "conv_state[%d]" % layer)
+                same_bits(ss, oss, "ssm_state[%d]" % layer)
+            harr = np.array(toks[-256:], np.int32)
+            a = m.step(int(toks[-1]), harr, 1.0)
+            b = O.orc_model_step(h, int(toks[-1]), ptr(harr), harr.size, 1.0)
+            same_bits(m.logits(), np.ctypeslib.as_array(O.orc_model_logits(h), (m.vocab,)),
+                      "logits after prefill %s" % parts)
+            assert a == b
+    finally:
+        O.orc_model_free(h)
+        m.free()
+
+
 def test_tiny_generate_matches_reference(hip):
     g = gold("tiny")
     blob, prompt, steps = model_image(g)
