@@ -9,7 +9,8 @@ one replay of the captured per-token hipGraph with inputs already in HBM.
 
 Prints ONE JSON line.  Legs (all by default):
   decode    W untimed steps, then K timed steps -> tok/s (the value) and
-            packed-weight GB/s
+            packed-weight GB/s; then the device prefill of a 1024-token
+            prompt on the same model (prefill_1b: time to first token)
   sampled   the same model decoding with the device sampler (temp 0.8,
             min_p 0.05, top_p 0.9, top_k 40): tok/s of up to 128 steps
   roofline  the decode GEMV kernel (K=2048 in_proj shape) streaming 512 MiB
@@ -116,6 +117,17 @@ def leg_decode(L, steps, warmup, sampled=False):
         sw = time.perf_counter() - t1
         samp = dict(SAMPLED, steps=n, tok_s=round(n / sw, 2), ms_per_step=round(sw * 1e3 / n, 4),
                     device_ms_per_step=round(sms / n, 4))
+    # time to first token: the device prefill of a 1024-token prompt
+    m.reset()
+    long_prompt = bh.synth_prompt(c["seed"] + 1, c["vocab"], 1024)
+    m.prefill(long_prompt[:16])
+    m.reset()
+    L.bm_hip_synchronize()
+    t2 = time.perf_counter()
+    m.prefill(long_prompt)
+    L.bm_hip_synchronize()
+    pf = time.perf_counter() - t2
+    prefill = dict(tokens=1024, ms=round(pf * 1e3, 3), tok_s=round(1024 / pf, 1))
     m.free()
     match = None
     gold = os.path.join(ROOT, "tests", "golden", "stream_1b.json")
@@ -123,7 +135,7 @@ def leg_decode(L, steps, warmup, sampled=False):
         ref = json.load(open(gold))["tokens"]
         n = min(len(ref), len(toks))
         match = toks[:n].tolist() == ref[:n]
-    return wall, dev_ms, match, samp
+    return wall, dev_ms, match, samp, prefill
 
 
 def leg_d255m(L):
@@ -514,9 +526,11 @@ def main():
         sys.exit("bm_hip_init: " + bh.last_error())
     res = {}
     if "decode" in legs:
-        wall, dev_ms, match, samp = leg_decode(L, a.steps, a.warmup, "sampled" in legs)
+        wall, dev_ms, match, samp, pf = leg_decode(L, a.steps, a.warmup, "sampled" in legs)
         res["decode"] = (wall, dev_ms, match)
         res["sampled"] = samp
+        res["prefill_model"] = pf
+        log("prefill: %s" % json.dumps(pf))
         log("decode: %d steps in %.2f ms wall (%.2f ms device)" % (a.steps, wall * 1e3, dev_ms))
         if samp:
             log("sampled decode: %s" % json.dumps(samp))
@@ -568,6 +582,7 @@ def main():
     else:
         line.update(value=None, ms_per_step=None)
     line["decode_sampled"] = res.get("sampled")
+    line["prefill_1b"] = res.get("prefill_model")
     line["roofline"] = roof
     line["mfma_ceiling"] = mf
     line["prefill_gemm"] = pre
