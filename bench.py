@@ -517,8 +517,8 @@ def main():
                     default="decode,sampled,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs on exactly one GPU (the BitLinear hot path at bs=1 "
-              "has no multi-GPU path); run with --gpus 1", file=sys.stderr)
+        print("bench.py: the BitLinear hot path runs on exactly one GPU (there is no "
+              "multi-GPU path at bs=1); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     legs = set(a.legs.split(","))
     L = bh.lib()

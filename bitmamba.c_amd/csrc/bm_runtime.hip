@@ -126,7 +126,7 @@ bool init_locked(Backend& b) {
   hipDeviceProp_t prop;
   BM_HIP_CHECK_RET(hipGetDeviceProperties(&prop, 0), false);
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
-    bm_set_error("device 0 is %s, this build targets gfx950 only", prop.gcnArchName);
+    bm_set_error("device 0 is %s, the library targets gfx950 only", prop.gcnArchName);
     return false;
   }
   BM_HIP_CHECK_RET(hipSetDevice(0), false);

@@ -4,7 +4,8 @@
  * A plain-C restatement of the reference's scalar path (jserv/bitmamba.c,
  * src/kernel.c, src/quantization.c, src/block.c, src/model.c).  Only the
  * tests, __graft_entry__.smoke() and the cpu_baseline leg of bench.py load
- * it, and only as the checker; the product library never links it.
+ * it, and only to check results or time the CPU; the product library never
+ * links it.
  *
  * Pinning (each function is checked by something other than itself):
  *   orc_luts / orc_decode_weight   exhaustive 256-byte KAT vs the compiled

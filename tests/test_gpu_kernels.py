@@ -3,8 +3,8 @@ fixtures, through the C ABI.
 
 Bar: int8, int32 and fp32 outputs bit-exact (the fp32 epilogue follows the
 scalar kernel's 1024-column block order, so no tolerance is needed; the
-north-star tolerance 1e-4 relative is asserted as a second, looser line in
-the fp32 tests so a failure shows how far off it is).
+stated 1e-4 relative tolerance is asserted as a second, looser line in the
+fp32 tests so a failure shows how far off it is).
 """
 import ctypes as C
 import os
