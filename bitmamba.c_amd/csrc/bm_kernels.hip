@@ -520,9 +520,10 @@ __global__ __launch_bounds__(256) void k_gemv_mt(const uint8_t* __restrict__ act
 }
 
 // ---------------------------------------------------------------------------
-// Few-token product on int8 MFMA (2 <= M <= 32, K % 128 == 0): the tokens
-// are the 32 rows of v_mfma_i32_32x32x32_i8's A operand (rows past M are
-// zeros and are not stored), 32 weight rows its B operand.  A block
+// Few-token product on int8 MFMA (2 <= M <= 256, K % 128 == 0): block row
+// y takes tokens 32y .. 32y+31, the 32 rows of v_mfma_i32_32x32x32_i8's A
+// operand (rows past M are zeros and are not stored); 32 weight rows are
+// its B operand.  A block
 // of 8 waves owns GPB groups of 32 weight rows; the WPG waves of a group
 // split its 1024-column slices.  Each wave loads a slice's packed weights
 // and the tokens' permuted int8 (cache-resident: every block reads them)
@@ -534,6 +535,7 @@ __global__ __launch_bounds__(256) void k_gemv_mt(const uint8_t* __restrict__ act
 // 128t + 64h + 16q .. in step q of each 128-column block t.
 // ---------------------------------------------------------------------------
 constexpr int kSmMaxM = 32, kSmMaxSlices = 16;  // K <= 16384
+constexpr int kSmMaxTokens = 256;  // up to 8 token tiles of 32 in one launch
 
 __host__ __device__ inline int sm_wpg(int n_slices) {  // waves per row group: a power of two
   return n_slices >= 8 ? 8 : (n_slices >= 4 ? 4 : (n_slices >= 2 ? 2 : 1));
@@ -547,6 +549,15 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
                                                     float w_scale, float* __restrict__ out,
                                                     int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
+  // token tile blockIdx.y: tokens 32y .. 32y+31
+  const int m_base = blockIdx.y * kSmMaxM;
+  act += (size_t)m_base * act_stride;
+  scale_x += m_base;
+  if (I32)
+    out_i32 += (size_t)m_base * N;
+  else
+    out += (size_t)m_base * N;
+  M = min(kSmMaxM, M - m_base);
   extern __shared__ __attribute__((aligned(16))) float s_part[];  // [slice][32 tokens][GPB*32 rows]
   __shared__ int s_sx[kSmMaxM][kSmMaxSlices];
   __shared__ float s_inv[kSmMaxM];
@@ -1067,15 +1078,6 @@ static hipError_t gemv_mt_t(const uint8_t* act, const float* scale_x, int M, con
 template <bool CANON, int MODE>
 static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
                                 int N, int K, float w_scale, void* out, hipStream_t s) {
-  if (M >= 2 && M <= kSmMaxM && K % 128 == 0 && K <= 16384) {
-    const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
-    const dim3 grid((N + 32 * gpb - 1) / (32 * gpb));
-    const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
-    hipLaunchKernelGGL((k_gemm_small<CANON, MODE>), grid, dim3(512), lds, s, act,
-                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
-                       (int32_t*)out);
-    return hipGetLastError();
-  }
   if (M >= 2 && M <= kMtMaxM && K <= kMtMaxK) {
     if (K <= 1024) return gemv_mt_t<16, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
     if (K <= 2048) return gemv_mt_t<32, 1, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
@@ -1110,23 +1112,47 @@ static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const 
 }
 
 // which kernel serves a product of this shape
-static int product_path(int M, int K) {
-  if (K % 64 != 0 || K > 16384) return 0;  // generic
-  if (M >= 32 && K % GBK == 0) return 2;   // MFMA GEMM
-  return 1;                                // GEMV per token
+// blocks of one k_gemm_small launch
+static long long small_blocks(int M, int N, int K) {
+  const int gpb = 8 / sm_wpg(slices_of(K));
+  return (long long)((N + 32 * gpb - 1) / (32 * gpb)) * ((M + kSmMaxM - 1) / kSmMaxM);
+}
+
+// which kernel serves a product of this shape: 0 generic, 1 GEMV per token,
+// 2 MFMA GEMM, 3 few-token MFMA.  Few tokens: up to 32 always; up to 256
+// while one launch fits one block per CU, where it measured faster than the
+// 128-row GEMM tiles (K=4096 -> 2048: 9-11 us against 23 us at M = 32-256;
+// K=2048 -> 8384: 9.5 us against 14 us at M = 32, 64)
+static int product_path(int M, int N, int K) {
+  if (K % 64 != 0 || K > 16384) return 0;
+  if (M >= 2 && K % 128 == 0 &&
+      (M <= kSmMaxM || (M <= kSmMaxTokens && small_blocks(M, N, K) <= 256)))
+    return 3;
+  if (M >= 32 && K % GBK == 0) return 2;
+  return 1;
 }
 
 template <bool CANON, int MODE>
 static hipError_t product_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
                             int N, int K, float w_scale, void* out, hipStream_t s) {
-  if (product_path(M, K) == 2) return gemm_t<CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  const int path = product_path(M, N, K);
+  if (path == 2) return gemm_t<CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+  if (path == 3) {
+    const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
+    const dim3 grid((N + 32 * gpb - 1) / (32 * gpb), (M + kSmMaxM - 1) / kSmMaxM);
+    const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
+    hipLaunchKernelGGL((k_gemm_small<CANON, MODE>), grid, dim3(512), lds, s, act,
+                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                       (int32_t*)out);
+    return hipGetLastError();
+  }
   return gemv_dispatch<CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
 }
 
 hipError_t launch_product(const uint8_t* act, const float* scale_x, int M, const uint8_t* packed,
                           int N, int K, float w_scale, bool canonical, void* out, int mode,
                           hipStream_t s) {
-  if (product_path(M, K) == 0) return hipErrorInvalidValue;  // caller uses launch_generic
+  if (product_path(M, N, K) == 0) return hipErrorInvalidValue;  // caller uses launch_generic
   if (canonical) {
     if (mode == MODE_I32) return product_t<true, 2>(act, scale_x, M, packed, N, K, w_scale, out, s);
     if (mode == MODE_ACC) return product_t<true, 1>(act, scale_x, M, packed, N, K, w_scale, out, s);
@@ -1137,7 +1163,7 @@ hipError_t launch_product(const uint8_t* act, const float* scale_x, int M, const
   return product_t<false, 0>(act, scale_x, M, packed, N, K, w_scale, out, s);
 }
 
-bool product_needs_generic(int M, int K) { return product_path(M, K) == 0; }
+bool product_needs_generic(int M, int K) { return product_path(M, 1, K) == 0; }
 
 hipError_t launch_generic(const int8_t* xq, int ldx, const float* scale_x, int M,
                           const uint8_t* packed, int N, int K, float w_scale, void* out, int mode,

@@ -178,7 +178,8 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (64, 4096, 64), (40, 8192, 129), (16, 8192, 512),
                                    (3, 1024, 50), (300, 1152, 260), (700, 2048, 1100),
                                    (1100, 1024, 700), (48, 16384, 96), (2, 2048, 77),
-                                   (31, 4096, 300), (5, 8192, 33)])
+                                   (31, 4096, 300), (5, 8192, 33), (97, 4096, 200),
+                                   (256, 2048, 64)])
 def test_gemm_i32_exact(hip, M, K, N):
     note("gemm i32 M=%d K=%d N=%d" % (M, K, N))
     r = rnd(M * 3 + K + N)
@@ -230,7 +231,10 @@ FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257)
              (48, 2048, 520), (40, 4096, 260),
              # few tokens on MFMA: 1, 2, 3, 4, 5 and 16 slices of 1024 columns
              (7, 2048, 8512), (16, 4096, 2048), (12, 3072, 100), (9, 5120, 64), (31, 1024, 70),
-             (30, 16384, 40)]
+             (30, 16384, 40),
+             # several token tiles of 32 (ragged last tile), and past the few-token range
+             (64, 2048, 8384), (100, 4096, 2048), (256, 4096, 2048), (77, 3072, 96),
+             (128, 2048, 8384)]
 
 
 @pytest.mark.parametrize("M,K,N", FP_SHAPES)
