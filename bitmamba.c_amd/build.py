@@ -17,8 +17,9 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
-    # parity: no a*b+c contraction anywhere in the device code
-    "-ffp-contract=off",
+    # parity: no a*b+c contraction anywhere in the device code, and fp32
+    # division as the correctly rounded IEEE sequence
+    "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     # packed fp32 instructions off (wrong results seen on this hardware)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",

@@ -761,7 +761,7 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 //   of x is subtracted at each 1024-column slice boundary, where the int32
 //   totals are folded into fp32 in slice order.
 // ---------------------------------------------------------------------------
-constexpr int GBM = 128, GBK = 128;  // tile rows and stage depth; columns: 64 * WN
+constexpr int GBM = 128, GBK = 128;  // largest tile rows and stage depth; columns: 64 * WN
 constexpr int GMAX_SLICES = 16;  // K <= 16384
 
 // Output tile of a block.  Workgroups go to the 8 XCDs round robin
@@ -789,8 +789,9 @@ struct GemmStage {
 
 // WN waves along N (2: 256 threads, tile 128 x 128, two blocks per CU;
 // 4: 512 threads, tile 128 x 256, one block per CU -- each A stage then
-// feeds twice the columns)
-template <bool CANON, int MODE, int WN>
+// feeds twice the columns); MT 32-row MFMA tiles per wave along M (2: 128
+// tile rows; 1: 64, for grids that 128-row tiles leave short of the CUs)
+template <bool CANON, int MODE, int WN, int MT>
 __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict__ act,
                                                  size_t act_stride,
                                                  const float* __restrict__ scale_x, int M,
@@ -799,30 +800,31 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
                                                  int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
   constexpr int GBN = 64 * WN, NT = 128 * WN;  // tile columns, threads
-  constexpr int NA = 8 / WN;                  // A chunks per thread per stage
+  constexpr int TBM = 64 * MT;                // tile rows
+  constexpr int NA = 4 * MT / WN;             // A chunks per thread per stage
   constexpr int BB = GBK / 4;                 // packed bytes per weight row per stage
-  __shared__ __attribute__((aligned(16))) uint8_t sA[3][GBM * GBK];
+  __shared__ __attribute__((aligned(16))) uint8_t sA[3][TBM * GBK];
   __shared__ __attribute__((aligned(16))) uint8_t sB[3][GBN * BB];
-  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][GBM];
-  __shared__ __attribute__((aligned(16))) float s_inv[GBM];
+  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][TBM];
+  __shared__ __attribute__((aligned(16))) float s_inv[TBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int j32 = lane & 31, h = lane >> 5;
   int tm, tn;
-  gemm_tile_of(blockIdx.x, (M + GBM - 1) / GBM, (N + GBN - 1) / GBN, tm, tn);
-  const int m0 = tm * GBM, n0 = tn * GBN;
+  gemm_tile_of(blockIdx.x, (M + TBM - 1) / TBM, (N + GBN - 1) / GBN, tm, tn);
+  const int m0 = tm * TBM, n0 = tn * GBN;
   const size_t wstride = (size_t)(K >> 2);
   const size_t perm = act_perm_off(K);
   const int n_slices = slices_of(K);
   const int n_stages = K / GBK;
 
   // per-row slice sums of x and 1/(scale_x * w_scale)
-  for (int i = tid; i < GBM * n_slices; i += NT) {
-    const int r = i % GBM, sl = i / GBM;
+  for (int i = tid; i < TBM * n_slices; i += NT) {
+    const int r = i % TBM, sl = i / TBM;
     const int row = min(m0 + r, M - 1);
     s_sx[sl][r] = ((const int*)(act + (size_t)row * act_stride))[sl];
   }
-  if (tid < GBM) {
+  if (tid < TBM) {
     const int row = min(m0 + tid, M - 1);
     s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[row], w_scale);
   }
@@ -852,10 +854,10 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
     *(v4i*)(sB[buf] + col * BB + 16 * ((tid & 1) ^ ((col >> 3) & 1))) = r.b;
   };
 
-  v16i acc[2][2];
-  float o[2][2][16];
+  v16i acc[MT][2];
+  float o[MT][2][16];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < MT; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -873,10 +875,10 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
     store_stage((st + 1) % 3, X);  // the buffer stage st-2 used
     const uint8_t* __restrict__ cA = sA[st % 3];
     const uint8_t* __restrict__ cB = sB[st % 3];
-    v4i aop[2][4];
+    v4i aop[MT][4];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int r = wm * 64 + mt * 32 + j32;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = wm * 32 * MT + mt * 32 + j32;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         aop[mt][q] = *(const v4i*)(cA + r * GBK + 16 * ((4 * h + q) ^ ((r >> 1) & 7)));
@@ -901,7 +903,7 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
         bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
           acc[mt][nt] =
@@ -912,11 +914,11 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
     if (!I32 && (((kb + GBK) % kSlice == 0) || st + 1 == n_stages)) {
       const int slice = kb / kSlice;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           // rows 8g + 4h + (0..3) of the tile: acc elements v = 4g .. 4g+3
-          const int rb = wm * 64 + mt * 32 + 8 * g + 4 * h;
+          const int rb = wm * 32 * MT + mt * 32 + 8 * g + 4 * h;
           const int4 sx4 = *(const int4*)&s_sx[slice][rb];
           const float4 in4 = *(const float4*)&s_inv[rb];
           const int sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
@@ -956,10 +958,10 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
   if (I32) {
     // exact totals: x.code over all of K minus the sum of x over all slices
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int rl = wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int rl = wm * 32 * MT + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         int sx = 0;
         for (int sl = 0; sl < n_slices; ++sl) sx += s_sx[sl][rl];
 #pragma unroll
@@ -968,13 +970,13 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
   }
 
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int n = n0 + wn * 64 + nt * 32 + j32;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int r = m0 + wm * 64 + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int r = m0 + wm * 32 * MT + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (r < M && n < N) {
           if (I32)
             out_i32[(size_t)r * N + n] = __float_as_int(o[mt][nt][v]);
@@ -1093,20 +1095,28 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
 
 // 128 x 256 tiles (one 512-thread block per CU) for products of at least
 // four rounds of them (measured 1.19x faster per tile at K=N=8192, M=4096);
-// 128 x 128 (two 256-thread blocks per CU) otherwise, where the finer grid
-// balances better
+// 64 x 128 where 128 x 128 tiles would not give every CU two blocks;
+// 128 x 128 (two 256-thread blocks per CU) otherwise
+constexpr int kGemmSlots = 512;  // 256 CUs x two 256-thread blocks
 template <bool CANON, int MODE>
 static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
                          int K, float w_scale, void* out, hipStream_t s) {
-  const int tm = (M + GBM - 1) / GBM;
-  if ((long long)tm * ((N + 255) / 256) >= 4 * 256) {
-    const dim3 grid(tm * ((N + 255) / 256));
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 4>), grid, dim3(512), 0, s, act, act_row_bytes(K),
-                       scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+  const long long tm = (M + GBM - 1) / GBM, tn = (N + 127) / 128;
+  if (tm * ((N + 255) / 256) >= 4 * 256) {
+    const dim3 grid((unsigned)(tm * ((N + 255) / 256)));
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, 4, 2>), grid, dim3(512), 0, s, act,
+                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                       (int32_t*)out);
+  } else if (tm * tn < kGemmSlots) {
+    const dim3 grid((unsigned)((M + 63) / 64 * tn));
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 1>), grid, dim3(256), 0, s, act,
+                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                       (int32_t*)out);
   } else {
-    const dim3 grid(tm * ((N + 127) / 128));
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 2>), grid, dim3(256), 0, s, act, act_row_bytes(K),
-                       scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+    const dim3 grid((unsigned)(tm * tn));
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 2>), grid, dim3(256), 0, s, act,
+                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                       (int32_t*)out);
   }
   return hipGetLastError();
 }

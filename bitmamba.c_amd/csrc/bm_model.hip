@@ -54,89 +54,174 @@ __device__ __forceinline__ float softplus_ref(float x) {
 // proj holds the in_proj outputs in the device's per-head order: head h
 // occupies [h*(2hd+3), (h+1)*(2hd+3)) of a token's row as
 // [z (hd) | x (hd) | B | C | dt].
-constexpr int kSsmChunk = 256;  // tokens per phase-1 pass
-enum { PRE_DECAY = 0, PRE_XBDT, PRE_C, PRE_XAD, PRE_SZ, PRE_COUNT };
-
-__global__ void k_ssm_prep(const float* __restrict__ proj, int pd, int t0, int nt, int di, int nh,
-                           int hd, const float* __restrict__ dt_bias, const float* __restrict__ A,
-                           const float* __restrict__ cw, const float* __restrict__ cb,
-                           const float* __restrict__ cs, const float* __restrict__ D,
-                           const int* __restrict__ ctl, float* __restrict__ pre) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
-  if (idx >= di || t >= nt) return;
-  const int tg = t0 + t;
-  const int h = idx / hd, c = idx - h * hd;
-  const size_t hoff = (size_t)h * (2 * hd + 3);
-  const float* __restrict__ ph = proj + (size_t)tg * pd + hoff;
-  const int pos0 = ctl[CTL_POS];
-  // input of token tg - k: from the batch, or from the conv ring for the
-  // three tokens before it (x_{-j} sits at ring position pos0 + 3 - j)
-  auto prev = [&](int k) {
-    const int tp = tg - k;
-    return tp >= 0 ? proj[(size_t)tp * pd + hoff + hd + c]
-                   : cs[(size_t)((pos0 + 3 + tp) % 3) * di + idx];
-  };
-  const float dt_val = softplus_ref(__fadd_rn(ph[2 * hd + 2], dt_bias[h]));
-  const float decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
-  const float Bdt = __fmul_rn(ph[2 * hd], dt_val);
-  const float xin = ph[hd + c];
-  float conv = __fadd_rn(cb[idx], __fmul_rn(prev(3), cw[idx]));
-  conv = __fadd_rn(conv, __fmul_rn(prev(2), cw[di + idx]));
-  conv = __fadd_rn(conv, __fmul_rn(prev(1), cw[2 * di + idx]));
-  conv = __fadd_rn(conv, __fmul_rn(xin, cw[3 * di + idx]));
-  const float xa = silu_ref(conv);
-  const size_t plane = (size_t)nt * di, at = (size_t)t * di + idx;
-  pre[PRE_DECAY * plane + at] = decay;
-  pre[PRE_XBDT * plane + at] = __fmul_rn(xa, Bdt);
-  pre[PRE_C * plane + at] = ph[2 * hd + 1];
-  pre[PRE_XAD * plane + at] = __fmul_rn(xa, D[idx]);
-  pre[PRE_SZ * plane + at] = silu_ref(ph[c]);
+constexpr int kSsmChunk = 1024;  // tokens per pass of the three phases
+// Phase values of a chunk of nt tokens, in nq = ceil(nt / 4) token quads.
+// The recurrence reads and writes per channel four tokens at a time, so its
+// planes keep a quad's four values together:
+//   XBDT  xa * B * dt   [nqa][di][4]   (phase 1 -> 2)
+//   ST    the state after each token [nqa][di][4]   (phase 2 -> 3)
+//   DECAY exp(A * dt)   [nh][nqa * 4]  (phase 1 -> 2)
+// and the rest per (token, channel) or (token, head):
+//   XAD   xa * D,  SZ  silu(z)  [nt][di]   (phase 1 -> 3)
+//   C     [nt][nh]                         (phase 1 -> 3)
+// The recurrence runs without conditions over nqr quads (nq rounded up to
+// whole pairs of its Q-quad buffers): tokens past nt carry decay 1 and
+// xa * B * dt = -0, which leave every state value, zeros' signs included,
+// as it is.  Its last prefetch reads Q quads further (nqa = nqr + Q).
+constexpr int kScanQ = 8, kScanQSmall = 4;
+__host__ __device__ inline int scan_q(int nq) { return nq <= 2 * kScanQSmall ? kScanQSmall : kScanQ; }
+struct PreLayout {
+  int nq, nqr, nqa;
+  size_t xbdt, st, decay, xad, sz, c, total;  // float offsets
+};
+__host__ __device__ inline PreLayout pre_layout(int nt, int di, int nh) {
+  PreLayout L;
+  L.nq = (nt + 3) / 4;
+  const int q = scan_q(L.nq);
+  L.nqr = (L.nq + 2 * q - 1) / (2 * q) * (2 * q);
+  L.nqa = L.nqr + q;
+  const size_t ch = (size_t)di, nq4 = (size_t)L.nqa * 4;
+  L.xbdt = 0;
+  L.st = L.xbdt + nq4 * ch;
+  L.decay = L.st + nq4 * ch;  // float4 reads: every offset up to here is a multiple of 4
+  L.xad = L.decay + (size_t)nh * nq4;
+  L.sz = L.xad + (size_t)nt * ch;
+  L.c = L.sz + (size_t)nt * ch;
+  L.total = L.c + (size_t)nt * nh;
+  return L;
 }
 
-// Phase 2 for tokens t0 .. t0+nt-1: the state recurrence alone, one thread
-// per channel, reading decay and xa * B * dt 32 tokens ahead; each token's
-// state goes to y, which phase 3 turns into the output.  The last chunk
-// (n_total > 0) also leaves the conv ring as the token loop would: the
+// Phase 1, one block per (256 channels, token quad) over the nqr quads:
+// the head values (dt, decay, B * dt) once per (token, head) of the block,
+// then per channel the conv over the quad's window of inputs, silu and the
+// products; tokens past the chunk get the recurrence's identity values
+__global__ __launch_bounds__(256) void k_ssm_prep(const float* __restrict__ proj, int pd, int t0,
+                                                  int nt, int di, int nh, int hd,
+                                                  const float* __restrict__ dt_bias,
+                                                  const float* __restrict__ A,
+                                                  const float* __restrict__ cw,
+                                                  const float* __restrict__ cb,
+                                                  const float* __restrict__ cs,
+                                                  const float* __restrict__ D,
+                                                  const int* __restrict__ ctl,
+                                                  float* __restrict__ pre) {
+  __shared__ float s_bdt[4][256];
+  const PreLayout PL = pre_layout(nt, di, nh);
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x, q = blockIdx.y, tq = 4 * q;
+  // the heads this block's channels belong to: h_first .. h_first + nhb - 1
+  const int h_first = (blockIdx.x * blockDim.x) / hd;
+  const int nhb = min(di - 1, (int)(blockIdx.x * blockDim.x + blockDim.x) - 1) / hd - h_first + 1;
+  for (int w = threadIdx.x; w < 4 * nhb; w += blockDim.x) {
+    const int e = w / nhb, hb = w - e * nhb, t = tq + e, h = h_first + hb;
+    float decay = 1.0f;
+    if (t < nt) {
+      const float* __restrict__ ph = proj + (size_t)(t0 + t) * pd + (size_t)h * (2 * hd + 3);
+      const float dt_val = softplus_ref(__fadd_rn(ph[2 * hd + 2], dt_bias[h]));
+      s_bdt[e][hb] = __fmul_rn(ph[2 * hd], dt_val);
+      decay = libm::expf_glibc(__fmul_rn(A[h], dt_val));
+      pre[PL.c + (size_t)t * nh + h] = ph[2 * hd + 1];
+    }
+    pre[PL.decay + (size_t)h * PL.nqa * 4 + t] = decay;
+  }
+  __syncthreads();
+  if (idx >= di) return;
+  const int h = idx / hd, c = idx - h * hd;
+  const size_t xoff = (size_t)h * (2 * hd + 3) + hd + c;
+  const int pos0 = ctl[CTL_POS];
+  // inputs of tokens tq-3 .. tq+3 of the chunk: from the batch, or from the
+  // conv ring for the three tokens before the prompt (x_{-j} sits at ring
+  // position pos0 + 3 - j); past the chunk's end: unused
+  float xv[7];
+#pragma unroll
+  for (int k = 0; k < 7; ++k) {
+    const int tp = tq - 3 + k, tg = t0 + tp;
+    xv[k] = tp >= nt ? 0.0f
+            : tg >= 0 ? proj[(size_t)tg * pd + xoff]
+                      : cs[(size_t)((pos0 + 3 + tg) % 3) * di + idx];
+  }
+  const float w0 = cw[idx], w1 = cw[di + idx], w2 = cw[2 * di + idx], w3 = cw[3 * di + idx];
+  const float bias = cb[idx], Dv = D[idx];
+  float xb[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = tq + e;
+    xb[e] = -0.0f;
+    if (t < nt) {
+      float conv = __fadd_rn(bias, __fmul_rn(xv[e], w0));
+      conv = __fadd_rn(conv, __fmul_rn(xv[e + 1], w1));
+      conv = __fadd_rn(conv, __fmul_rn(xv[e + 2], w2));
+      conv = __fadd_rn(conv, __fmul_rn(xv[e + 3], w3));
+      const float xa = silu_ref(conv);
+      xb[e] = __fmul_rn(xa, s_bdt[e][h - h_first]);
+      const size_t at = (size_t)t * di + idx;
+      pre[PL.xad + at] = __fmul_rn(xa, Dv);
+      pre[PL.sz + at] = silu_ref(proj[(size_t)(t0 + t) * pd + xoff - hd]);
+    }
+  }
+  reinterpret_cast<float4*>(pre + PL.xbdt)[(size_t)q * di + idx] =
+      make_float4(xb[0], xb[1], xb[2], xb[3]);
+}
+
+// Phase 2 for the chunk's tokens: the state recurrence alone, one thread per
+// channel, a quad of tokens per load, two buffers of Q quads in flight and
+// no branch in the loop, so loads wait only for their own buffer.  The last
+// chunk (n_total > 0) also leaves the conv ring as the token loop would: the
 // inputs of the last three tokens at their ring positions.
-__global__ __launch_bounds__(64) void k_ssm_scan(const float* __restrict__ pre, int t0, int nt,
-                                                 int di, float* __restrict__ ssm,
-                                                 float* __restrict__ y,
+template <int Q>
+__global__ __launch_bounds__(64) void k_ssm_scan(float* __restrict__ pre, int nt, int di, int nh,
+                                                 float* __restrict__ ssm,
                                                  const float* __restrict__ proj, int pd, int hd,
                                                  float* __restrict__ cs,
                                                  const int* __restrict__ ctl, int n_total) {
-  constexpr int B = 32;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= di) return;
-  const size_t plane = (size_t)nt * di;
+  const PreLayout PL = pre_layout(nt, di, nh);
+  const int h = idx / hd;
+  const float4* __restrict__ xbq = reinterpret_cast<const float4*>(pre + PL.xbdt) + idx;
+  const float4* __restrict__ decq =
+      reinterpret_cast<const float4*>(pre + PL.decay + (size_t)h * PL.nqa * 4);
+  float4* __restrict__ stq = reinterpret_cast<float4*>(pre + PL.st) + idx;
   float st = ssm[idx];
-  float dec[2][B], xb[2][B];
-  auto fetch = [&](int buf, int tb) __attribute__((always_inline)) {
+  float4 dec[2][Q], xb[2][Q];
+  auto fetch = [&](int buf, int qb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < B; ++j) {
-      const bool in = tb + j < nt;
-      const size_t at = (size_t)(tb + j) * di + idx;
-      dec[buf][j] = in ? pre[PRE_DECAY * plane + at] : 0.0f;
-      xb[buf][j] = in ? pre[PRE_XBDT * plane + at] : 0.0f;
+    for (int j = 0; j < Q; ++j) {
+      dec[buf][j] = decq[qb + j];
+      xb[buf][j] = xbq[(size_t)(qb + j) * di];
     }
   };
-  auto run = [&](int buf, int tb) __attribute__((always_inline)) {
+  auto run = [&](int buf, int qb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < B; ++j)
-      if (tb + j < nt) {
-        st = __fadd_rn(__fmul_rn(st, dec[buf][j]), xb[buf][j]);
-        y[(size_t)(t0 + tb + j) * di + idx] = st;
-      }
+    for (int j = 0; j < Q; ++j) {
+      const float4 d = dec[buf][j], x = xb[buf][j];
+      float4 o;
+      st = __fadd_rn(__fmul_rn(st, d.x), x.x);
+      o.x = st;
+      st = __fadd_rn(__fmul_rn(st, d.y), x.y);
+      o.y = st;
+      st = __fadd_rn(__fmul_rn(st, d.z), x.z);
+      o.z = st;
+      st = __fadd_rn(__fmul_rn(st, d.w), x.w);
+      o.w = st;
+      stq[(size_t)(qb + j) * di] = o;
+    }
   };
+  // the scheduler barriers keep each buffer's loads ahead of the other's
+  // updates, as written
   fetch(0, 0);
-  for (int tb = 0; tb < nt; tb += 2 * B) {
-    fetch(1, tb + B);  // past nt: zeros, not used
-    run(0, tb);
-    fetch(0, tb + 2 * B);
-    run(1, tb + B);
+  for (int qb = 0; qb < PL.nqr; qb += 2 * Q) {
+    fetch(1, qb + Q);
+    __builtin_amdgcn_sched_barrier(0);
+    run(0, qb);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(0, qb + 2 * Q);  // past nqr on the last pass: read, not used
+    __builtin_amdgcn_sched_barrier(0);
+    run(1, qb + Q);
+    __builtin_amdgcn_sched_barrier(0);
   }
   ssm[idx] = st;
   if (n_total > 0) {
-    const int h = idx / hd, c = idx - h * hd;
+    const int c = idx - h * hd;
     const int pos0 = ctl[CTL_POS];
     for (int k = max(0, n_total - 3); k < n_total; ++k)
       cs[(size_t)((pos0 + k) % 3) * di + idx] =
@@ -144,16 +229,26 @@ __global__ __launch_bounds__(64) void k_ssm_scan(const float* __restrict__ pre, 
   }
 }
 
-// Phase 3: y = (st * C + xa * D) * silu(z) for every (token, channel) of
-// the chunk, st being the state phase 2 left in y
-__global__ void k_ssm_out(const float* __restrict__ pre, int t0, int nt, int di,
-                          float* __restrict__ y) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
-  if (idx >= di || t >= nt) return;
-  const size_t plane = (size_t)nt * di, at = (size_t)t * di + idx;
-  float* __restrict__ yp = y + (size_t)(t0 + t) * di + idx;
-  *yp = __fmul_rn(__fadd_rn(__fmul_rn(*yp, pre[PRE_C * plane + at]), pre[PRE_XAD * plane + at]),
-                  pre[PRE_SZ * plane + at]);
+// Phase 3, one thread per (channel, token quad): y = (st * C + xa * D) *
+// silu(z) with st the state phase 2 left after each token
+__global__ __launch_bounds__(256) void k_ssm_out(const float* __restrict__ pre, int t0, int nt,
+                                                 int di, int nh, int hd, float* __restrict__ y) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x, q = blockIdx.y;
+  if (idx >= di) return;
+  const PreLayout PL = pre_layout(nt, di, nh);
+  const int h = idx / hd;
+  const float4 s4 = reinterpret_cast<const float4*>(pre + PL.st)[(size_t)q * di + idx];
+  const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = 4 * q + e;
+    if (t < nt) {
+      const size_t at = (size_t)t * di + idx;
+      y[(size_t)(t0 + t) * di + idx] =
+          __fmul_rn(__fadd_rn(__fmul_rn(sv[e], pre[PL.c + (size_t)t * nh + h]), pre[PL.xad + at]),
+                    pre[PL.sz + at]);
+    }
+  }
 }
 
 __global__ void k_advance_pos(int* ctl, int n) {
@@ -308,7 +403,7 @@ struct bm_hip_model {
   int8_t* xq = nullptr;
   // prefill scratch (grow on demand)
   float *px = nullptr, *pproj = nullptr, *py = nullptr, *pscale = nullptr;
-  float* ppre = nullptr;  // prefill SSM phase-1 values, PRE_COUNT planes of a chunk
+  float* ppre = nullptr;  // prefill SSM phase-1 values of a chunk (pre_layout)
   uint8_t* pact = nullptr;
   int8_t* pxq = nullptr;
   int* ptok = nullptr;
@@ -465,8 +560,8 @@ int ensure_prefill(bm_hip_model* m, int n) {
   MCHECK(hipMalloc(&m->pact, (size_t)n * bm::act_row_bytes((int)K)));
   MCHECK(hipMalloc(&m->pxq, (size_t)n * K));
   MCHECK(hipMalloc(&m->ptok, (size_t)n * 4));
-  MCHECK(hipMalloc(&m->ppre, (size_t)bm::PRE_COUNT * (n < bm::kSsmChunk ? n : bm::kSsmChunk) *
-                                 m->di * 4));
+  MCHECK(hipMalloc(&m->ppre,
+                   bm::pre_layout(n < bm::kSsmChunk ? n : bm::kSsmChunk, m->di, m->nh).total * 4));
   m->pcap = n;
   return 0;
 }
@@ -750,16 +845,19 @@ extern "C" int bm_hip_model_prefill(bm_hip_model_t* m, const int32_t* tokens, in
     float* cs = m->conv_state + (size_t)l * 3 * di;
     for (int t0 = 0; t0 < n; t0 += bm::kSsmChunk) {
       const int nt = n - t0 < bm::kSsmChunk ? n - t0 : bm::kSsmChunk;
-      hipLaunchKernelGGL(bm::k_ssm_prep, dim3((di + 255) / 256, nt), dim3(256), 0, s, m->pproj,
-                         m->pd, t0, nt, di, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt,
-                         Ly.conv_b, cs, Ly.D, m->ctl, m->ppre);
+      const bm::PreLayout PL = bm::pre_layout(nt, di, m->nh);
+      hipLaunchKernelGGL(bm::k_ssm_prep, dim3((di + 255) / 256, PL.nqr), dim3(256), 0, s,
+                         m->pproj, m->pd, t0, nt, di, m->nh, m->hd, Ly.dt_bias, Ly.A,
+                         Ly.conv_wt, Ly.conv_b, cs, Ly.D, m->ctl, m->ppre);
       MCHECK(hipGetLastError());
-      hipLaunchKernelGGL(bm::k_ssm_scan, dim3((di + 63) / 64), dim3(64), 0, s, m->ppre, t0, nt,
-                         di, m->ssm_state + (size_t)l * di, m->py, m->pproj, m->pd, m->hd, cs,
-                         m->ctl, t0 + nt == n ? n : 0);
+      auto scan = bm::scan_q(PL.nq) == bm::kScanQ ? bm::k_ssm_scan<bm::kScanQ>
+                                                  : bm::k_ssm_scan<bm::kScanQSmall>;
+      hipLaunchKernelGGL(scan, dim3((di + 63) / 64), dim3(64), 0, s, m->ppre, nt, di, m->nh,
+                         m->ssm_state + (size_t)l * di, m->pproj, m->pd, m->hd, cs, m->ctl,
+                         t0 + nt == n ? n : 0);
       MCHECK(hipGetLastError());
-      hipLaunchKernelGGL(bm::k_ssm_out, dim3((di + 255) / 256, nt), dim3(256), 0, s, m->ppre, t0,
-                         nt, di, m->py);
+      hipLaunchKernelGGL(bm::k_ssm_out, dim3((di + 255) / 256, PL.nq), dim3(256), 0, s, m->ppre,
+                         t0, nt, di, m->nh, m->hd, m->py);
       MCHECK(hipGetLastError());
     }
     if (bitlinear(m, m->py, n, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->px,
@@ -953,18 +1051,35 @@ extern "C" int bm_hip_model_tokens(const bm_hip_model_t* m, int32_t* out, int n)
   return n;
 }
 
-// Diagnostic: evaluates the device libm restatement (fn 0 = expf, 1 = logf).
+// Diagnostic: evaluates the device scalar functions of the SSM path: fn 0
+// expf, 1 logf, 2 the division of each even/odd pair of inputs (both
+// orders: out[i] = in[i] / in[i ^ 1]), 3 silu.
 namespace bm {
 __global__ void k_libm_eval(int fn, const float* __restrict__ in, float* __restrict__ out,
                             size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x)
-    out[i] = fn == 0 ? libm::expf_glibc(in[i]) : libm::logf_glibc(in[i]);
+       i += (size_t)gridDim.x * blockDim.x) {
+    const float v = in[i];
+    float r;
+    if (fn == 0)
+      r = libm::expf_glibc(v);
+    else if (fn == 1)
+      r = libm::logf_glibc(v);
+    else if (fn == 2)
+      r = cr_divf(v, in[(i ^ 1) < n ? (i ^ 1) : i]);
+    else
+      r = silu_ref(v);
+    out[i] = r;
+  }
 }
 }  // namespace bm
 
 extern "C" int bm_hip_libm_eval_dev(int fn, const float* in, float* out, size_t n, void* stream) {
   if (!bm_hip_init()) return -1;
+  if (fn < 0 || fn > 3) {
+    bm_set_error("bm_hip_libm_eval_dev: fn must be 0..3");
+    return -1;
+  }
   int blocks = (int)((n + 255) / 256);
   if (blocks > 8192) blocks = 8192;
   if (blocks < 1) blocks = 1;

@@ -60,6 +60,44 @@ def test_device_libm(hip):
         same_bits(got, ref, name)
 
 
+def test_device_division_and_silu(hip):
+    """Device fp32 division and silu against the host's IEEE float arithmetic
+    (numpy float32, and the oracle's glibc expf inside silu): 2^24 pairs of
+    every-exponent bit patterns (zeros, subnormals, infinities included) and
+    of the ranges the sampler, the norms and the SSM divide in."""
+    note("device division and silu")
+    r = np.random.default_rng(2)
+    bits = r.integers(0, 1 << 32, 1 << 23, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45, 1.1754942e-38,
+                         1.1754944e-38, 3.4028235e38, -3.4028235e38, 1.0, -1.0, 127.0,
+                         1e-5, 20.0, 255.0], np.float32)
+    pairs = np.stack(np.meshgrid(specials, specials), -1).reshape(-1)
+    dense = np.concatenate([r.uniform(-30, 30, 1 << 22), r.uniform(1e-6, 100, 1 << 22),
+                            r.uniform(-1, 1, 1 << 21)]).astype(np.float32)
+    x = np.concatenate([pairs, bits, dense]).astype(np.float32)
+    x = x[: x.size // 2 * 2]
+    x = x[~np.isnan(x).reshape(-1, 2).any(1).repeat(2)]
+    dx = bh.DeviceBuffer.from_array(x)
+    dy = bh.DeviceBuffer(x.nbytes)
+    O = native.oracle()
+    with np.errstate(all="ignore"):
+        partner = x.reshape(-1, 2)[:, ::-1].reshape(-1)
+        ref_div = (x / partner).astype(np.float32)
+        e = np.empty_like(x)
+        O.orc_expf_array(ptr(np.ascontiguousarray(-x)), ptr(e), x.size)
+        ref_silu = (x / (np.float32(1.0) + e)).astype(np.float32)
+    for fn, name, ref in ((2, "division", ref_div), (3, "silu", ref_silu)):
+        bh.check(hip.bm_hip_libm_eval_dev(fn, dx.ptr, dy.ptr, x.size, None), name)
+        hip.bm_hip_synchronize()
+        got = dy.download(x.shape, np.float32)
+        ref = ref.copy()
+        both_nan = np.isnan(got) & np.isnan(ref)
+        got[both_nan] = 0
+        ref[both_nan] = 0
+        same_bits(got, ref, name)
+    assert hip.bm_hip_libm_eval_dev(4, dx.ptr, dy.ptr, x.size, None) == -1
+
+
 def _oracle_model(blob):
     O = native.oracle()
     h = O.orc_model_load(ptr(blob), blob.nbytes)
@@ -145,16 +183,18 @@ def test_wide_model_logits_vs_oracle(hip, d_model, n_heads, penalty):
 
 def test_prefill_lengths_vs_oracle(hip):
     """Prefill in one call and in several (the conv ring and the state carry
-    over), with 1 to 600 tokens (several 256-token chunks of the two-phase
-    SSM): every layer's state and the next step's logits bit-exact against
-    the oracle's token-serial prefill."""
+    over), with 1 to 2050 tokens (several 1024-token chunks of the
+    three-phase SSM, counts that are not whole 4-token quads): every layer's
+    state and the next step's logits bit-exact against the oracle's
+    token-serial prefill."""
     g = gold("tiny")
     blob, _, _ = model_image(g)
     c = g["config"]
     m = bh.Model(blob)
     O, h = _oracle_model(blob)
     try:
-        for parts in ([1], [2], [3], [5], [300], [600], [100, 200], [1, 2, 257]):
+        for parts in ([1], [2], [3], [5], [300], [600], [100, 200], [1, 2, 257], [1025],
+                      [2050], [7, 1030]):
             note("prefill parts %s" % parts)
             m.reset()
             O.orc_model_free(h)
