@@ -1093,27 +1093,46 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
   return gemv_t<64, 4, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
 }
 
-// 128 x 256 tiles (one 512-thread block per CU) for products of at least
-// four rounds of them (measured 1.19x faster per tile at K=N=8192, M=4096);
-// 64 x 128 where 128 x 128 tiles would not give every CU two blocks;
-// 128 x 128 (two 256-thread blocks per CU) otherwise
-constexpr int kGemmSlots = 512;  // 256 CUs x two 256-thread blocks
+// Tile shape per product: the one with the least estimated time, in rounds
+// of resident blocks weighted by the measured cost of a full round of each
+// shape relative to 128 x 128 (two 256-thread blocks per CU): 128 x 256
+// (one 512-thread block per CU) 0.85, 64 x 128 0.58 (M=4096, K=4096->2048:
+// 40.4 / 47.3 / 27.5 us per round at M=4096 / 4096 / 2048).  A last round
+// that leaves at most one block per CU of a two-per-CU grid counts 0.6 (a
+// block alone on its CU runs faster).  The estimate orders the measured
+// times of all three shapes at M=1024..4096 for K=2048->8512 and
+// K=4096->2048.
+constexpr int kCUs = 256;
+static double rounds_cost(long long tiles, int slots, bool two_per_cu) {
+  const long long full = tiles / slots, rest = tiles % slots;
+  return (double)full + (rest == 0 ? 0.0 : (two_per_cu && rest <= slots / 2) ? 0.6 : 1.0);
+}
+enum { GEMM_64x128 = 0, GEMM_128x128 = 1, GEMM_128x256 = 2 };
+static int gemm_shape(int M, int N) {
+  const long long tn128 = (N + 127) / 128, tn256 = (N + 255) / 256;
+  const double c64 = 0.58 * rounds_cost((M + 63) / 64 * tn128, 2 * kCUs, true);
+  const double c128 = rounds_cost((M + 127) / 128 * tn128, 2 * kCUs, true);
+  const double c256 = 0.85 * rounds_cost((M + 127) / 128 * tn256, kCUs, false);
+  if (c256 <= c128 && c256 <= c64) return GEMM_128x256;
+  return c64 < c128 ? GEMM_64x128 : GEMM_128x128;
+}
+
 template <bool CANON, int MODE>
 static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
                          int K, float w_scale, void* out, hipStream_t s) {
-  const long long tm = (M + GBM - 1) / GBM, tn = (N + 127) / 128;
-  if (tm * ((N + 255) / 256) >= 4 * 256) {
-    const dim3 grid((unsigned)(tm * ((N + 255) / 256)));
+  const int shape = gemm_shape(M, N);
+  if (shape == GEMM_128x256) {
+    const dim3 grid((unsigned)((M + 127) / 128 * ((N + 255) / 256)));
     hipLaunchKernelGGL((k_gemm<CANON, MODE, 4, 2>), grid, dim3(512), 0, s, act,
                        act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
                        (int32_t*)out);
-  } else if (tm * tn < kGemmSlots) {
-    const dim3 grid((unsigned)((M + 63) / 64 * tn));
+  } else if (shape == GEMM_64x128) {
+    const dim3 grid((unsigned)((M + 63) / 64 * ((N + 127) / 128)));
     hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 1>), grid, dim3(256), 0, s, act,
                        act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
                        (int32_t*)out);
   } else {
-    const dim3 grid((unsigned)(tm * tn));
+    const dim3 grid((unsigned)((M + 127) / 128 * ((N + 127) / 128)));
     hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 2>), grid, dim3(256), 0, s, act,
                        act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
                        (int32_t*)out);

@@ -179,7 +179,9 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (3, 1024, 50), (300, 1152, 260), (700, 2048, 1100),
                                    (1100, 1024, 700), (48, 16384, 96), (2, 2048, 77),
                                    (31, 4096, 300), (5, 8192, 33), (97, 4096, 200),
-                                   (256, 2048, 64)])
+                                   (256, 2048, 64),
+                                   # the three GEMM tile shapes: 64x128, 128x128, 128x256
+                                   (1233, 256, 8512), (2100, 128, 2048), (1920, 256, 8512)])
 def test_gemm_i32_exact(hip, M, K, N):
     note("gemm i32 M=%d K=%d N=%d" % (M, K, N))
     r = rnd(M * 3 + K + N)
@@ -253,20 +255,21 @@ def test_bitlinear_fp32_exact(hip, M, K, N):
 
 
 def test_prefill_shapes_sampled(hip):
-    """Prefill GEMM shapes M=2048: K=2048->N=8512 and K=4096->N=2048, fp32,
+    """Prefill GEMM shapes M=2048: K=2048->N=8512 and K=4096->N=2048 (and
+    M=1233, 1024 of the 1B prefill, which take the other tile shapes), fp32,
     activations N(0,1) with 1% outliers x10; 40 token rows (first/last tile
     included) checked bit-exactly against the oracle."""
     r = rnd(2048)
-    for K, N, seed in ((2048, 8512, 11), (4096, 2048, 12)):
-        note("prefill M=2048 K=%d N=%d" % (K, N))
-        M = 2048
+    for M, K, N, seed in ((2048, 2048, 8512, 11), (2048, 4096, 2048, 12),
+                          (1233, 2048, 8512, 13), (1024, 2048, 8384, 14)):
+        note("prefill M=%d K=%d N=%d" % (M, K, N))
         packed = bh.synth_ternary(seed, 1, N, K, bh.SYNTH_UNIFORM)
         x = bh.synth_normal(seed, 2, (M, K), 1.0)
         mask = r.random((M, K)) < 0.01
         x[mask] *= 10.0
         g = np.ones(K, np.float32)
         out, xq = gpu_bitlinear(hip, x, packed, N, K, 0.02, g, canonical=1)
-        rows = np.unique(np.concatenate([[0, 1, 127, 128, M - 1], r.integers(0, M, 35)]))
+        rows = np.unique(np.concatenate([[0, 1, 63, 64, 127, 128, M - 1], r.integers(0, M, 35)]))
         ref, _, rq = native.orc_bitlinear(x[rows], packed, N, K, 0.02, g)
         np.testing.assert_array_equal(xq[rows], rq)
         same_bits(out[rows], ref, "out[rows]")
