@@ -1051,9 +1051,9 @@ extern "C" int bm_hip_model_tokens(const bm_hip_model_t* m, int32_t* out, int n)
   return n;
 }
 
-// Diagnostic: evaluates the device scalar functions of the SSM path: fn 0
-// expf, 1 logf, 2 the division of each even/odd pair of inputs (both
-// orders: out[i] = in[i] / in[i ^ 1]), 3 silu.
+// Diagnostic: evaluates the device scalar functions of the SSM path and the
+// norms: fn 0 expf, 1 logf, 2 the division of each even/odd pair of inputs
+// (both orders: out[i] = in[i] / in[i ^ 1]), 3 silu, 4 sqrt.
 namespace bm {
 __global__ void k_libm_eval(int fn, const float* __restrict__ in, float* __restrict__ out,
                             size_t n) {
@@ -1067,8 +1067,10 @@ __global__ void k_libm_eval(int fn, const float* __restrict__ in, float* __restr
       r = libm::logf_glibc(v);
     else if (fn == 2)
       r = cr_divf(v, in[(i ^ 1) < n ? (i ^ 1) : i]);
-    else
+    else if (fn == 3)
       r = silu_ref(v);
+    else
+      r = cr_sqrtf(v);
     out[i] = r;
   }
 }
@@ -1076,8 +1078,8 @@ __global__ void k_libm_eval(int fn, const float* __restrict__ in, float* __restr
 
 extern "C" int bm_hip_libm_eval_dev(int fn, const float* in, float* out, size_t n, void* stream) {
   if (!bm_hip_init()) return -1;
-  if (fn < 0 || fn > 3) {
-    bm_set_error("bm_hip_libm_eval_dev: fn must be 0..3");
+  if (fn < 0 || fn > 4) {
+    bm_set_error("bm_hip_libm_eval_dev: fn must be 0..4");
     return -1;
   }
   int blocks = (int)((n + 255) / 256);

@@ -344,8 +344,8 @@ int bm_hip_model_tokens(const bm_hip_model_t *m, int32_t *out, int n);
  * functions of the SSM step on n device floats, for checks against the host:
  * fn 0 = expf, 1 = logf (restatements of glibc's), 2 = fp32 division of each
  * even/odd input pair in both orders (out[i] = in[i] / in[i ^ 1]; a last
- * unpaired input is divided by itself), 3 = silu, x / (1 + expf(-x)).
- * Returns -1 for any other fn. */
+ * unpaired input is divided by itself), 3 = silu, x / (1 + expf(-x)),
+ * 4 = sqrt.  Returns -1 for any other fn. */
 int bm_hip_libm_eval_dev(int fn,
                          const float *in,
                          float *out,

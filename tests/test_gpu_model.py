@@ -60,11 +60,11 @@ def test_device_libm(hip):
         same_bits(got, ref, name)
 
 
-def test_device_division_and_silu(hip):
-    """Device fp32 division and silu against the host's IEEE float arithmetic
-    (numpy float32, and the oracle's glibc expf inside silu): 2^24 pairs of
-    every-exponent bit patterns (zeros, subnormals, infinities included) and
-    of the ranges the sampler, the norms and the SSM divide in."""
+def test_device_division_sqrt_and_silu(hip):
+    """Device fp32 division, sqrt and silu against the host's IEEE float
+    arithmetic (numpy float32, and the oracle's glibc expf inside silu): 2^24
+    pairs of every-exponent bit patterns (zeros, subnormals, infinities
+    included) and of the ranges the sampler, the norms and the SSM use."""
     note("device division and silu")
     r = np.random.default_rng(2)
     bits = r.integers(0, 1 << 32, 1 << 23, dtype=np.uint64).astype(np.uint32).view(np.float32)
@@ -86,7 +86,8 @@ def test_device_division_and_silu(hip):
         e = np.empty_like(x)
         O.orc_expf_array(ptr(np.ascontiguousarray(-x)), ptr(e), x.size)
         ref_silu = (x / (np.float32(1.0) + e)).astype(np.float32)
-    for fn, name, ref in ((2, "division", ref_div), (3, "silu", ref_silu)):
+        ref_sqrt = np.sqrt(x).astype(np.float32)
+    for fn, name, ref in ((2, "division", ref_div), (3, "silu", ref_silu), (4, "sqrt", ref_sqrt)):
         bh.check(hip.bm_hip_libm_eval_dev(fn, dx.ptr, dy.ptr, x.size, None), name)
         hip.bm_hip_synchronize()
         got = dy.download(x.shape, np.float32)
@@ -95,7 +96,7 @@ def test_device_division_and_silu(hip):
         got[both_nan] = 0
         ref[both_nan] = 0
         same_bits(got, ref, name)
-    assert hip.bm_hip_libm_eval_dev(4, dx.ptr, dy.ptr, x.size, None) == -1
+    assert hip.bm_hip_libm_eval_dev(5, dx.ptr, dy.ptr, x.size, None) == -1
 
 
 def _oracle_model(blob):
