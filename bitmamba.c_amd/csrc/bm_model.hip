@@ -47,8 +47,8 @@ __device__ __forceinline__ float softplus_ref(float x) {
 // depend on the previous token; dt, decay, the depthwise conv over the
 // token's three predecessors, silu and the products with B * dt and D do
 // not.  Phase 1 computes those for a chunk of tokens with one thread per
-// (token, channel); phase 2 runs the recurrence, one thread per channel;
-// phase 3 forms y from each token's state, again in parallel.
+// (channel, 4-token quad); phase 2 runs the recurrence, one thread per
+// channel; phase 3 forms y from each token's state, again in parallel.
 // Every value is the same fp32 expression, in the same order, as in the
 // token-serial loop, so the results are bit for bit those of that loop.
 // proj holds the in_proj outputs in the device's per-head order: head h
