@@ -182,6 +182,43 @@ def test_wide_model_logits_vs_oracle(hip, d_model, n_heads, penalty):
         m.free()
 
 
+# GEMM tiles of the 1B width: 300 tokens 64x128, 1220 in_proj 128x128, 2100
+# 128x256 (three SSM chunks); 255M width, 1030 tokens: in_proj 128x256,
+# out_proj 64x128, two SSM chunks
+@pytest.mark.parametrize("d_model,n_heads,n_tokens", [(1024, 32, 1030), (2048, 64, 300),
+                                                      (2048, 64, 1220), (2048, 64, 2100)])
+def test_wide_model_long_prefill_vs_oracle(hip, d_model, n_heads, n_tokens):
+    """Long prompts at the 255M and 1B widths (two layers, 2000-token
+    vocabulary): the batched path with MFMA GEMM tiles, the quantize kernels
+    at K = 1024 .. 4096 and, at 1030 tokens, two chunks of the three-phase
+    SSM with 64-channel heads.  Every state value and the next step's logits
+    bit-exact against the oracle's token-serial prefill."""
+    note("wide model long prefill d_model=%d tokens=%d" % (d_model, n_tokens))
+    blob = bh.synth_model(2000, d_model, 2, n_heads, 91 + d_model, bh.SYNTH_UNIFORM)
+    prompt = bh.synth_prompt(91, 2000, n_tokens + 1)
+    m = bh.Model(blob)
+    O, h = _oracle_model(blob)
+    try:
+        p = prompt[:-1].copy()
+        m.prefill(p)
+        O.orc_model_prefill(h, ptr(p), p.size)
+        for layer in range(m.n_layers):
+            cs, ss, pos = m.layer_state(layer)
+            ocs = np.empty((3, m.d_inner), np.float32)
+            oss = np.empty(m.d_inner, np.float32)
+            assert pos == O.orc_model_layer_state(h, layer, ptr(ocs), ptr(oss))
+            same_bits(cs, ocs, "conv_state[%d]" % layer)
+            same_bits(ss, oss, "ssm_state[%d]" % layer)
+        harr = np.array(prompt[-256:], np.int32)
+        a = m.step(int(prompt[-1]), harr, 1.0)
+        b = O.orc_model_step(h, int(prompt[-1]), ptr(harr), harr.size, 1.0)
+        same_bits(m.logits(), np.ctypeslib.as_array(O.orc_model_logits(h), (m.vocab,)), "logits")
+        assert a == b
+    finally:
+        O.orc_model_free(h)
+        m.free()
+
+
 def test_prefill_lengths_vs_oracle(hip):
     """Prefill in one call and in several (the conv ring and the state carry
     over), with 1 to 2050 tokens (several 1024-token chunks of the
