@@ -46,10 +46,12 @@ extern "C" void bm_set_error(const char *fmt, ...);
 // error; shapes are validated by the callers.
 namespace bm {
 
+// nibbles = false leaves the split-nibble part of the workspace unwritten
+// (for products that read only the permuted bytes: product_reads_nibbles)
 hipError_t launch_quantize(const float *x, int M, int n, int x_stride,
                            const float *gamma, float *x_norm, int8_t *xq,
                            int quant_stride, float *scale_x, uint8_t *act,
-                           hipStream_t s);
+                           hipStream_t s, bool nibbles = true);
 hipError_t launch_prep_i8(const int8_t *xq, int M, int ldx, int K, uint8_t *act,
                           hipStream_t s);
 // Output modes of the products: fp32 store, fp32 accumulate (out += o, the
@@ -62,6 +64,7 @@ hipError_t launch_product(const uint8_t *act, const float *scale_x, int M,
                           const uint8_t *packed, int N, int K, float w_scale,
                           bool canonical, void *out, int mode, hipStream_t s);
 bool product_needs_generic(int M, int K);
+bool product_reads_nibbles(int M, int N, int K);
 hipError_t launch_generic(const int8_t *xq, int ldx, const float *scale_x,
                           int M, const uint8_t *packed, int N, int K,
                           float w_scale, void *out, int mode, hipStream_t s);

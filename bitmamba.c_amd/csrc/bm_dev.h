@@ -24,9 +24,11 @@ __device__ __forceinline__ uint32_t canon_codes(uint32_t p) {
 // Activation workspace writers
 // ---------------------------------------------------------------------------
 
-// 16 int8 values of columns 16g..16g+15 -> split nibbles + permuted int8
+// 16 int8 values of columns 16g..16g+15 -> split nibbles (unless nib is
+// false: the MFMA products read only the permuted bytes) + permuted int8
 __device__ __forceinline__ void write_act_group(uint8_t* __restrict__ act_row, int K, int g,
-                                                const int (&q)[16]) {
+                                                const int (&q)[16], bool nib = true) {
+  if (nib) {
   uint32_t le = 0, lo = 0, he = 0, ho = 0;
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
@@ -36,8 +38,8 @@ __device__ __forceinline__ void write_act_group(uint8_t* __restrict__ act_row, i
     he |= (uint32_t)((xe >> 4) & 15) << (4 * n);
     ho |= (uint32_t)((xo >> 4) & 15) << (4 * n);
   }
-  uint4 nib = make_uint4(le, lo, he, ho);
-  *(uint4*)(act_row + act_nib_off(K) + 16 * (size_t)g) = nib;
+  *(uint4*)(act_row + act_nib_off(K) + 16 * (size_t)g) = make_uint4(le, lo, he, ho);
+  }
   uint32_t pm[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
                                                        int8_t* __restrict__ xq, int quant_stride,
                                                        float* __restrict__ scale_out,
                                                        uint8_t* __restrict__ act,
-                                                       size_t act_stride) {
+                                                       size_t act_stride, bool nib) {
   constexpr int K = 1024 * G, E = K / 64;
   extern __shared__ __attribute__((aligned(16))) float lds_sq[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
         for (int j = 0; j < 16; ++j) dst[j] = (int8_t)q[j];
       }
     }
-    if (arow) write_act_group(arow, K, g, q);
+    if (arow) write_act_group(arow, K, g, q, nib);
     const int ssum = wave_sum_i32(qsum);  // groups 64i .. 64i+63 = slice i
     if (arow && lane == 0) ((int*)arow)[i] = ssum;
   }
@@ -1004,7 +1004,7 @@ __global__ void k_canonicalize_tail(uint8_t* __restrict__ p, size_t n) {
 // ---------------------------------------------------------------------------
 hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const float* gamma,
                            float* x_norm, int8_t* xq, int quant_stride, float* scale_x,
-                           uint8_t* act, hipStream_t s) {
+                           uint8_t* act, hipStream_t s, bool nibbles) {
   if (M <= 0) return hipSuccess;
   // one wave per token when the rows allow 16-byte loads of whole groups
   const bool aligned = ((uintptr_t)x % 16 == 0) && (x_stride % 4 == 0) &&
@@ -1015,13 +1015,13 @@ hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const flo
     const size_t lds = quantize_wave_lds(n);
     if (n == 1024)
       hipLaunchKernelGGL(k_quantize_wave<1>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
-                         xq, quant_stride, scale_x, act, act_row_bytes(n));
+                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles);
     else if (n == 2048)
       hipLaunchKernelGGL(k_quantize_wave<2>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
-                         xq, quant_stride, scale_x, act, act_row_bytes(n));
+                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles);
     else
       hipLaunchKernelGGL(k_quantize_wave<4>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
-                         xq, quant_stride, scale_x, act, act_row_bytes(n));
+                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_quantize, dim3(M), dim3(QT), 0, s, x, n, x_stride, gamma, x_norm, xq,
@@ -1193,6 +1193,11 @@ hipError_t launch_product(const uint8_t* act, const float* scale_x, int M, const
 }
 
 bool product_needs_generic(int M, int K) { return product_path(M, 1, K) == 0; }
+
+bool product_reads_nibbles(int M, int N, int K) {
+  const int path = product_path(M, N, K);
+  return path != 2 && path != 3;
+}
 
 hipError_t launch_generic(const int8_t* xq, int ldx, const float* scale_x, int M,
                           const uint8_t* packed, int N, int K, float w_scale, void* out, int mode,

@@ -445,7 +445,7 @@ int bitlinear(bm_hip_model* m, const float* x, int M, int K, const float* norm,
               float* sc, int8_t* xq, hipStream_t s) {
   const bool generic = bm::product_needs_generic(M, K);
   MCHECK(bm::launch_quantize(x, M, K, K, norm, nullptr, generic ? xq : nullptr, K, sc,
-                             generic ? nullptr : act, s));
+                             generic ? nullptr : act, s, bm::product_reads_nibbles(M, N, K)));
   if (generic)
     MCHECK(bm::launch_generic(xq, K, sc, M, W, N, K, scale, out, mode, s));
   else
