@@ -62,7 +62,8 @@ constexpr int kSsmChunk = 1024;  // tokens per pass of the three phases
 //   ST    the state after each token [nqa][di][4]   (phase 2 -> 3)
 //   DECAY exp(A * dt)   [nh][nqa * 4]  (phase 1 -> 2)
 // and the rest per (token, channel) or (token, head):
-//   XAD   xa * D,  SZ  silu(z)  [nt][di]   (phase 1 -> 3)
+//   XAD   xa * D  [nt][di]   (phase 1 -> 3; phase 3 takes silu(z) itself,
+//         which balances the two: phase 1 is VALU-bound, phase 3 memory-bound)
 //   C     [nt][nh]                         (phase 1 -> 3)
 // The recurrence runs without conditions over nqr quads (nq rounded up to
 // whole pairs of its Q-quad buffers): tokens past nt carry decay 1 and
@@ -72,7 +73,7 @@ constexpr int kScanQ = 8, kScanQSmall = 4;
 __host__ __device__ inline int scan_q(int nq) { return nq <= 2 * kScanQSmall ? kScanQSmall : kScanQ; }
 struct PreLayout {
   int nq, nqr, nqa;
-  size_t xbdt, st, decay, xad, sz, c, total;  // float offsets
+  size_t xbdt, st, decay, xad, c, total;  // float offsets
 };
 __host__ __device__ inline PreLayout pre_layout(int nt, int di, int nh) {
   PreLayout L;
@@ -85,8 +86,7 @@ __host__ __device__ inline PreLayout pre_layout(int nt, int di, int nh) {
   L.st = L.xbdt + nq4 * ch;
   L.decay = L.st + nq4 * ch;  // float4 reads: every offset up to here is a multiple of 4
   L.xad = L.decay + (size_t)nh * nq4;
-  L.sz = L.xad + (size_t)nt * ch;
-  L.c = L.sz + (size_t)nt * ch;
+  L.c = L.xad + (size_t)nt * ch;
   L.total = L.c + (size_t)nt * nh;
   return L;
 }
@@ -155,7 +155,6 @@ __global__ __launch_bounds__(256) void k_ssm_prep(const float* __restrict__ proj
       xb[e] = __fmul_rn(xa, s_bdt[e][h - h_first]);
       const size_t at = (size_t)t * di + idx;
       pre[PL.xad + at] = __fmul_rn(xa, Dv);
-      pre[PL.sz + at] = silu_ref(proj[(size_t)(t0 + t) * pd + xoff - hd]);
     }
   }
   reinterpret_cast<float4*>(pre + PL.xbdt)[(size_t)q * di + idx] =
@@ -231,12 +230,15 @@ __global__ __launch_bounds__(64) void k_ssm_scan(float* __restrict__ pre, int nt
 
 // Phase 3, one thread per (channel, token quad): y = (st * C + xa * D) *
 // silu(z) with st the state phase 2 left after each token
-__global__ __launch_bounds__(256) void k_ssm_out(const float* __restrict__ pre, int t0, int nt,
-                                                 int di, int nh, int hd, float* __restrict__ y) {
+__global__ __launch_bounds__(256) void k_ssm_out(const float* __restrict__ pre,
+                                                 const float* __restrict__ proj, int pd, int t0,
+                                                 int nt, int di, int nh, int hd,
+                                                 float* __restrict__ y) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x, q = blockIdx.y;
   if (idx >= di) return;
   const PreLayout PL = pre_layout(nt, di, nh);
   const int h = idx / hd;
+  const size_t zoff = (size_t)h * (2 * hd + 3) + (idx - h * hd);
   const float4 s4 = reinterpret_cast<const float4*>(pre + PL.st)[(size_t)q * di + idx];
   const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(256) void k_ssm_out(const float* __restrict__ pre, 
       const size_t at = (size_t)t * di + idx;
       y[(size_t)(t0 + t) * di + idx] =
           __fmul_rn(__fadd_rn(__fmul_rn(sv[e], pre[PL.c + (size_t)t * nh + h]), pre[PL.xad + at]),
-                    pre[PL.sz + at]);
+                    silu_ref(proj[(size_t)(t0 + t) * pd + zoff]));
     }
   }
 }
@@ -857,7 +859,7 @@ extern "C" int bm_hip_model_prefill(bm_hip_model_t* m, const int32_t* tokens, in
                          t0 + nt == n ? n : 0);
       MCHECK(hipGetLastError());
       hipLaunchKernelGGL(bm::k_ssm_out, dim3((di + 255) / 256, PL.nq), dim3(256), 0, s, m->ppre,
-                         t0, nt, di, m->nh, m->hd, m->py);
+                         m->pproj, m->pd, t0, nt, di, m->nh, m->hd, m->py);
       MCHECK(hipGetLastError());
     }
     if (bitlinear(m, m->py, n, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->px,
