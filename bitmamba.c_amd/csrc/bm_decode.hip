@@ -435,6 +435,15 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
     }
   }
 
+  // MODE 1: the residual values of the prefetched rows, read now so that
+  // the final x += o does not wait for them
+  float resid[NPF];
+#pragma unroll
+  for (int it = 0; it < NPF; ++it) {
+    const int r = (g0 + wave + 4 * it) * RPW + sub;
+    resid[it] = (MODE == 1 && u == 0 && g0 + wave + 4 * it < g1 && r < N) ? out[r] : 0.0f;
+  }
+
   const Lds l = lds_carve(lds, K);
   float scale_x;
   if constexpr (WP) {
@@ -459,11 +468,11 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   float best_v = PICK == 2 ? -1e30f : -1e9f;
   int best_i = 0x7fffffff;
   const float inv_temp = PICK == 2 ? cr_divf(1.0f, temp) : 1.0f;
-  auto emit = [&](int r, float o) {
+  auto emit = [&](int r, float o, float res) {
     if (u == 0 && r < N) {
       if (PICK == 2) o = __fmul_rn(o, inv_temp);
       if (MODE == 1)
-        out[r] = __fadd_rn(out[r], o);
+        out[r] = __fadd_rn(res, o);
       else
         out[r] = o;
       if (PICK && o > best_v) {  // rows ascend per lane: first max kept
@@ -480,7 +489,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
 #pragma unroll
       for (int p = 0; p < P; ++p)
         o = row_finish<T>(dot64(wv[it][p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
-      emit(grp * RPW + sub, o);
+      emit(grp * RPW + sub, o, resid[it]);
     }
   }
   for (int grp = g0 + wave + 4 * NPF; grp < g1; grp += 4) {  // beyond the prefetch
@@ -493,7 +502,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
                                             : make_uint4(0, 0, 0, 0);
       o = row_finish<T>(dot64(w, xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
     }
-    emit(r, o);
+    emit(r, o, MODE == 1 && u == 0 && r < N ? out[r] : 0.0f);
   }
 
   if constexpr (PICK == 2) {
