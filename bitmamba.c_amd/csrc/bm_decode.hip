@@ -723,6 +723,11 @@ __global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
   __shared__ int si[4];
   __shared__ int s_tok;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the step counters, read while the candidates load (nothing else in the
+  // step writes them)
+  const int step = tid == 0 ? ctl[CTL_STEP] : 0;
+  const int hcount = tid == 0 ? ctl[CTL_HCOUNT] : 0;
+  const int pos = tid == 0 ? ctl[CTL_POS] : 0;
   float bv = -1e9f;
   int bi = 0x7fffffff;
   for (int b = tid; b < n_parts; b += blockDim.x) {
@@ -754,13 +759,12 @@ __global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
         bi = si[k];
       }
     const int best = bi == 0x7fffffff ? 0 : bi;
-    const int step = ctl[CTL_STEP];
     if (out_tokens) out_tokens[step] = best;
     ctl[CTL_STEP] = step + 1;
     ctl[CTL_TOKEN] = best;
-    hist[ctl[CTL_HCOUNT] % kHist] = best;
-    ctl[CTL_HCOUNT] += 1;
-    ctl[CTL_POS] = ctl[CTL_POS] + 1 < 3 ? ctl[CTL_POS] + 1 : 0;  // src/block.c:107
+    hist[hcount % kHist] = best;
+    ctl[CTL_HCOUNT] = hcount + 1;
+    ctl[CTL_POS] = pos + 1 < 3 ? pos + 1 : 0;  // src/block.c:107
     s_tok = best;
   }
   __syncthreads();

@@ -527,20 +527,36 @@ __device__ double ordered_sum(const Cand* __restrict__ c, int n, Smem& sm) {
 
 // the generator state back, then the step bookkeeping of k_argmax_step
 // (or, without ctl, the token alone); one thread
-__device__ void finish_step(int token, uint64_t rng, uint64_t* rng_state, const StepIO& io) {
+// the step counters, read by thread 0 when the kernel starts (nothing else
+// in the step writes them) so that the bookkeeping at its end waits for no
+// load
+struct CtlSnap {
+  int step = 0, hcount = 0, pos = 0;
+};
+__device__ __forceinline__ CtlSnap ctl_snap(const StepIO& io) {
+  CtlSnap c;
+  if (threadIdx.x == 0 && io.ctl) {
+    c.step = io.ctl[kCtlStep];
+    c.hcount = io.ctl[kCtlHcount];
+    c.pos = io.ctl[kCtlPos];
+  }
+  return c;
+}
+
+__device__ void finish_step(int token, uint64_t rng, uint64_t* rng_state, const StepIO& io,
+                            const CtlSnap& c) {
   *rng_state = rng;
   if (!io.ctl) {
     io.out_tokens[0] = token;
     return;
   }
   int* ctl = io.ctl;
-  const int step = ctl[kCtlStep];
-  if (io.out_tokens) io.out_tokens[step] = token;
-  ctl[kCtlStep] = step + 1;
+  if (io.out_tokens) io.out_tokens[c.step] = token;
+  ctl[kCtlStep] = c.step + 1;
   ctl[kCtlToken] = token;
-  io.hist[ctl[kCtlHcount] % kHist] = token;
-  ctl[kCtlHcount] += 1;
-  ctl[kCtlPos] = ctl[kCtlPos] + 1 < 3 ? ctl[kCtlPos] + 1 : 0;  // src/block.c:107
+  io.hist[c.hcount % kHist] = token;
+  ctl[kCtlHcount] = c.hcount + 1;
+  ctl[kCtlPos] = c.pos + 1 < 3 ? c.pos + 1 : 0;  // src/block.c:107
 }
 
 // the next token's embedding row (src/model.c:1116-1122), whole block
@@ -692,6 +708,7 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
   const Scratch sc = scratch_of(scratch, V);
   const int seg = front_seg(V);
   // every load that does not depend on another goes out first
+  const CtlSnap cs = ctl_snap(io);
   const int wave = threadIdx.x >> 6;
   int hc0 = 0, hc1 = 0;
   if (threadIdx.x < 64) {
@@ -826,7 +843,7 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
   if (threadIdx.x == 0) sm.iwork[4] = token;
   __syncthreads();
   token = sm.iwork[4];
-  if (threadIdx.x == 0) finish_step(token, rng, rng_state, io);
+  if (threadIdx.x == 0) finish_step(token, rng, rng_state, io, cs);
   embed_next(token, io);
   if (threadIdx.x < kBuckets) sc.hist[threadIdx.x] = 0;
 }
@@ -836,8 +853,9 @@ __global__ __launch_bounds__(1024) void k_sample_greedy(const float* __restrict_
                                                         uint64_t* __restrict__ rng_state,
                                                         StepIO io) {
   __shared__ Smem sm;
+  const CtlSnap cs = ctl_snap(io);
   const int token = argmax_scan(logits, V, -1e9f, sm);
-  if (threadIdx.x == 0) finish_step(token, *rng_state, rng_state, io);
+  if (threadIdx.x == 0) finish_step(token, *rng_state, rng_state, io, cs);
   embed_next(token, io);
 }
 
