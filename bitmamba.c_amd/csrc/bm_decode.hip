@@ -654,23 +654,35 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   }
   __syncthreads();
 
-  if (tid < kCB) {
-    // scalar_ssm_inner for channel idx (src/kernel.c:34-70)
-    const float dt_val = softplus_r(__fadd_rn(s_proj[2 * kCB + 2], dtb));
-    const float decay = libm::expf_glibc(__fmul_rn(Ah, dt_val));
-    const float Bdt = __fmul_rn(s_proj[2 * kCB], dt_val);
-    const float C_val = s_proj[2 * kCB + 1];
+  // scalar_ssm_inner for the block's channels (src/kernel.c:34-70), its
+  // three independent transcendental parts on three waves at once: wave 0
+  // the conv and silu(conv) of each channel, wave 1 silu(z), wave 2 the
+  // head's softplus and decay; then wave 0 forms the state and y
+  __shared__ float s_tail[2 * kCB + 2];
+  if (wave == 0 && lane < kCB) {
     const float xin = s_proj[kCB + c];
     float conv = __fadd_rn(cbias, __fmul_rn(tap0, cw0));
     conv = __fadd_rn(conv, __fmul_rn(tap1, cw1));
     conv = __fadd_rn(conv, __fmul_rn(tap2, cw2));
     conv = __fadd_rn(conv, __fmul_rn(xin, cw3));
     a.cs[(size_t)pos * a.di + idx] = xin;  // the oldest tap is overwritten
-    const float xact = silu_r(conv);
+    s_tail[c] = silu_r(conv);
+  } else if (wave == 1 && lane < kCB) {
+    s_tail[kCB + lane] = silu_r(s_proj[lane]);
+  } else if (wave == 2 && lane == 0) {
+    const float dt_val = softplus_r(__fadd_rn(s_proj[2 * kCB + 2], dtb));
+    s_tail[2 * kCB] = dt_val;
+    s_tail[2 * kCB + 1] = libm::expf_glibc(__fmul_rn(Ah, dt_val));
+  }
+  __syncthreads();
+  if (tid < kCB) {
+    const float dt_val = s_tail[2 * kCB], decay = s_tail[2 * kCB + 1];
+    const float Bdt = __fmul_rn(s_proj[2 * kCB], dt_val);
+    const float C_val = s_proj[2 * kCB + 1];
+    const float xact = s_tail[c];
     const float st = __fadd_rn(__fmul_rn(st0, decay), __fmul_rn(xact, Bdt));
     a.ssm[idx] = st;
-    a.y[idx] =
-        __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xact, Dc)), silu_r(s_proj[c]));
+    a.y[idx] = __fmul_rn(__fadd_rn(__fmul_rn(st, C_val), __fmul_rn(xact, Dc)), s_tail[kCB + c]);
   }
 }
 
