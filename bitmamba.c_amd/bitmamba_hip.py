@@ -81,6 +81,8 @@ SIGNATURES = {
     "bm_hip_bitlinear_act_dev": (_i, [_vp, _vp, _i, _vp, _i, _i, _f, _i, _vp, _vp]),
     "bm_hip_bitlinear_dev": (_i, [_vp, _i, _i, _vp, _vp, _i, _f, _i, _vp, _vp, _i, _vp, _vp,
                                   _vp]),
+    "bm_hip_bitlinear_noalloc_dev": (_i, [_vp, _i, _i, _vp, _vp, _i, _f, _i, _vp, _vp]),
+    "bm_hip_noalloc_scratch_bytes": (_sz, []),
     "bm_hip_i8_act_bytes": (_sz, [_i, _i]),
     "bm_hip_ternary_gemm_i32_dev": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "bm_hip_tiled_bytes": (_sz, [_i, _i]),

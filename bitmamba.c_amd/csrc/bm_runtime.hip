@@ -31,7 +31,17 @@ extern "C" void bm_set_error(const char* fmt, ...) {
 
 extern "C" const char* bm_hip_last_error(void) { return g_err; }
 
+// Scratch of the allocation-free entry point bm_hip_bitlinear_noalloc_dev:
+// a file-scope device array (each GPU holds its own copy until the process
+// ends).  In host code `scratch` names a host-side stand-in, never device
+// memory: kernels and copies get the address that hipGetSymbolAddress
+// returns at set-up (Backend::scratch_dev).
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 16;
 
 // calls whose inputs and outputs fit here skip the DMA copies: the kernels
 // read x from, and write their results to, mapped host memory
@@ -63,6 +73,8 @@ struct Backend {
   // pinned host staging (copies), and mapped coherent host memory that
   // the kernels of small calls read and write directly
   DevBuf h_stage, h_zc;
+  // device address of `scratch` on each device the library set up
+  void* scratch_dev[kMaxDevices] = {};
 };
 
 Backend& B() {
@@ -132,6 +144,10 @@ bool init_locked(Backend& b) {
   BM_HIP_CHECK_RET(hipSetDevice(0), false);
   BM_HIP_CHECK_RET(hipStreamCreateWithFlags(&b.stream, hipStreamNonBlocking), false);
   b.device = 0;
+  // with device 0 current: the address of its copy of `scratch`
+  void* sp = nullptr;
+  BM_HIP_CHECK_RET(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)), false);
+  b.scratch_dev[0] = sp;
   b.ready = true;
   return true;
 }
@@ -557,6 +573,61 @@ extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
                    -1);
   return 0;
 }
+
+// Quantize + product like bm_hip_bitlinear_dev, with the workspace (per-token
+// scale, activation workspace or int8 copy) in the file-scope scratch array
+// instead of caller or library allocations: no hipMalloc, hipFree or other
+// allocating call, so callers that cannot allocate (code under stream
+// capture, serving loops) can use it.  Calls that overlap on one GPU share
+// the array and race.
+extern "C" int bm_hip_bitlinear_noalloc_dev(const float* x, int M, int K, const float* norm_w,
+                                            const uint8_t* packed, int N, float w_scale,
+                                            int canonical, float* out, void* stream) {
+  Backend& b = B();
+  uint8_t* base = nullptr;
+  hipStream_t s = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(b.mu);
+    if (!b.ready) {
+      bm_set_error("bitlinear_noalloc: call bm_hip_init first (this entry point allocates "
+                   "nothing, the stream and scratch address included)");
+      return -1;
+    }
+    base = (uint8_t*)b.scratch_dev[b.device];
+    s = stream ? (hipStream_t)stream : b.stream;
+  }
+  if (M < 1 || N <= 0 || K <= 0 || !x || !norm_w || !packed || !out || !base) {
+    bm_set_error("bitlinear_noalloc: invalid arguments (M=%d N=%d K=%d)", M, N, K);
+    return -2;
+  }
+  const bool generic = bm::product_needs_generic(M, K);
+  // [scale_x (M floats) | activation workspace, or the int8 copy for K the
+  // products cover only through the generic kernel]
+  const size_t o_work = bm::align_up((size_t)M * 4, 256);
+  const size_t work = generic ? (size_t)M * (size_t)K : (size_t)M * bm::act_row_bytes(K);
+  const size_t need = o_work + work;
+  if (need > kScratchBytes) {
+    bm_set_error("bitlinear_noalloc: M=%d K=%d needs %zu bytes of scratch, the limit is %zu",
+                 M, K, need, kScratchBytes);
+    return -2;
+  }
+  float* sc = (float*)base;
+  uint8_t* wk = base + o_work;
+  BM_HIP_CHECK_RET(bm::launch_quantize(x, M, K, K, norm_w, nullptr, generic ? (int8_t*)wk : nullptr,
+                                       K, sc, generic ? nullptr : wk, s),
+                   -1);
+  if (generic)
+    BM_HIP_CHECK_RET(bm::launch_generic((const int8_t*)wk, K, sc, M, packed, N, K, w_scale, out,
+                                        bm::MODE_STORE, s),
+                     -1);
+  else
+    BM_HIP_CHECK_RET(bm::launch_product(wk, sc, M, packed, N, K, w_scale, canonical != 0, out,
+                                        bm::MODE_STORE, s),
+                     -1);
+  return 0;
+}
+
+extern "C" size_t bm_hip_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" size_t bm_hip_tiled_bytes(int N, int K) {
   if (N <= 0 || K <= 0 || K % 128 != 0) return 0;

@@ -218,6 +218,27 @@ int bm_hip_bitlinear_dev(const float *x,
                          void *act,
                          void *stream);
 
+/* No counterpart in the reference: bm_hip_bitlinear_dev without any
+ * allocation, for callers that cannot allocate (code under HIP stream
+ * capture, tight serving loops).  The per-token scale and the activation
+ * workspace (or int8 copy) live in a device array of the library's own,
+ * bm_hip_noalloc_scratch_bytes() = 8 MiB per GPU, held until the process
+ * ends; a call needing more (M * (K-row workspace) beyond it) returns -2.
+ * Needs bm_hip_init() first (-1 otherwise).  Calls that overlap on one GPU
+ * share the array and race.  Same semantics and output as
+ * bm_hip_bitlinear_dev (out[m*N + r], bit-exact). */
+int bm_hip_bitlinear_noalloc_dev(const float *x,
+                                 int M,
+                                 int K,
+                                 const float *norm_w,
+                                 const uint8_t *packed,
+                                 int N,
+                                 float w_scale,
+                                 int canonical,
+                                 float *out,
+                                 void *stream);
+size_t bm_hip_noalloc_scratch_bytes(void);
+
 /* Exact int32 product of int8 activations and ternary weights:
  * out[m*N + r] = sum_k xq[m*ldx + k] * decode(W[r][k]) (stress shape;
  * activations need no quantization).  M = 1 runs the decode GEMV, larger M
