@@ -696,7 +696,7 @@ __global__ void k_ssm_heads(const float* __restrict__ proj, int hd, int di,
                             float* __restrict__ cs, float* __restrict__ ssm,
                             const float* __restrict__ D, float* __restrict__ y,
                             const int* __restrict__ ctl) {
-  const int h = blockIdx.x, c = threadIdx.x;
+  const int h = blockIdx.x, c = blockIdx.y * blockDim.x + threadIdx.x;
   if (c >= hd) return;
   const float* __restrict__ ph = proj + (size_t)h * (2 * hd + 3);
   const int idx = h * hd + c;
@@ -845,6 +845,9 @@ hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8
 
 bool inproj_ssm_fits(int K, int hd) { return K % 64 == 0 && K <= 8192 && hd % kCB == 0; }
 
+// the shapes the fused row kernels (in_proj, out_proj, LM head) cover
+bool rows_fit(int K) { return K % 64 == 0 && K <= 8192; }
+
 // in_proj + SSM for every head: y (and the states) updated in one launch
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
@@ -881,10 +884,10 @@ hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const ui
 hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
                             const float* A, const float* cw, const float* cb, float* cs,
                             float* ssm, const float* D, float* y, const int* ctl, hipStream_t s) {
-  if (hd > 1024) return hipErrorInvalidValue;
-  const int threads = (hd + 63) / 64 * 64;
-  hipLaunchKernelGGL(k_ssm_heads, dim3(nh), dim3(threads), 0, s, proj, hd, nh * hd, dt_bias, A,
-                     cw, cb, cs, ssm, D, y, ctl);
+  // a block row per head, 256 channels per block
+  const int threads = hd < 256 ? (hd + 63) / 64 * 64 : 256;
+  hipLaunchKernelGGL(k_ssm_heads, dim3(nh, (hd + threads - 1) / threads), dim3(threads), 0, s,
+                     proj, hd, nh * hd, dt_bias, A, cw, cb, cs, ssm, D, y, ctl);
   return hipGetLastError();
 }
 

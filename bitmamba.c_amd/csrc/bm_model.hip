@@ -347,6 +347,7 @@ hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
                           float w_scale, float* x, hipStream_t s);
 bool inproj_ssm_fits(int K, int hd);
+bool rows_fit(int K);
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
                              const float* cw, const float* cb, float* cs, float* ssm,
@@ -458,9 +459,12 @@ int bitlinear(bm_hip_model* m, const float* x, int M, int K, const float* norm,
 
 
 // The kernels of one decode step, enqueued on s.  m->x already holds the
-// embedding of the current token.
+// embedding of the current token.  Widths the fused row kernels do not cover
+// (d_model % 64 != 0, more than 8192 columns) take the generic quantize +
+// product kernels instead, with the same results.
 int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) {
   const int dm = m->dm, di = m->di;
+  const bool rows_dm = bm::rows_fit(dm), rows_di = bm::rows_fit(di);
   for (int l = 0; l < m->nl; ++l) {
     const Layer& Ly = m->L[l];
     float* cs = m->conv_state + (size_t)l * 3 * di;
@@ -471,21 +475,39 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
                                    Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
                                    m->ctl, s));
     } else {
-      MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
-                               s));
+      if (rows_dm) {
+        MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
+                                 s));
+      } else if (bitlinear(m, m->x, 1, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
+                           bm::MODE_STORE, m->act, m->scale, m->xq, s)) {
+        return -1;
+      }
       MCHECK(bm::launch_ssm_heads(m->proj, m->nh, m->hd, Ly.dt_bias, Ly.A, Ly.conv_wt,
                                   Ly.conv_b, cs, ss, Ly.D, m->y, m->ctl, s));
     }
-    MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s));
+    if (rows_di) {
+      MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s));
+    } else if (bitlinear(m, m->y, 1, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x,
+                         bm::MODE_ACC, m->act, m->scale, m->xq, s)) {
+      return -1;
+    }
   }
   const bool sampled = !(m->temp < 0.05f);  // src/model.c:143-144
-  const bool fused_pick = penalty == 1.0f && !sampled;  // x / 1.0f == x * 1.0f == x
-  // sampled without a penalty: the LM head scales by 1/temp itself and
-  // hands its blocks' maxima to the sampler
-  const bool fused_scale = penalty == 1.0f && sampled;
-  MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab, m->lm_scale,
-                            m->logits, fused_pick ? 1 : (fused_scale ? 2 : 0), m->temp,
-                            m->part_v, m->part_i, s));
+  // the fused LM head: greedy candidates per block, or (sampled without a
+  // penalty) logits x 1/temp with the blocks' maxima
+  const bool fused_pick = rows_dm && penalty == 1.0f && !sampled;  // x / 1.0f == x * 1.0f == x
+  const bool fused_scale = rows_dm && penalty == 1.0f && sampled;
+  if (rows_dm) {
+    MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab,
+                              m->lm_scale, m->logits, fused_pick ? 1 : (fused_scale ? 2 : 0),
+                              m->temp, m->part_v, m->part_i, s));
+  } else {
+    // rms_norm(norm_f), then BitLinear with lm_head.norm (src/model.c:1225, 1259-1261)
+    MCHECK(bm::launch_rms_norm(m->x, dm, m->norm_f, m->feat, m->scale + 8, s));
+    if (bitlinear(m, m->feat, 1, dm, m->lm_norm, m->lm_head, m->vocab, m->lm_scale, m->logits,
+                  bm::MODE_STORE, m->act, m->scale, m->xq, s))
+      return -1;
+  }
   int* out = write_out ? m->out_tokens : nullptr;
   if (sampled) {
     if (penalty != 1.0f) {
@@ -551,9 +573,14 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
 
 int ensure_prefill(bm_hip_model* m, int n) {
   if (n <= m->pcap) return 0;
-  for (void* p : {(void*)m->px, (void*)m->pproj, (void*)m->py, (void*)m->pscale,
-                  (void*)m->pact, (void*)m->pxq, (void*)m->ptok, (void*)m->ppre})
-    if (p) (void)hipFree(p);
+  // free the old buffers and forget them first, so that a failed
+  // allocation below leaves no stale pointer and no capacity behind
+  m->pcap = 0;
+  for (void** p : {(void**)&m->px, (void**)&m->pproj, (void**)&m->py, (void**)&m->pscale,
+                   (void**)&m->pact, (void**)&m->pxq, (void**)&m->ptok, (void**)&m->ppre}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
   const size_t K = (size_t)(m->di > m->dm ? m->di : m->dm);
   MCHECK(hipMalloc(&m->px, (size_t)n * m->dm * 4));
   MCHECK(hipMalloc(&m->pproj, (size_t)n * m->pd * 4));
@@ -564,7 +591,7 @@ int ensure_prefill(bm_hip_model* m, int n) {
   MCHECK(hipMalloc(&m->ptok, (size_t)n * 4));
   MCHECK(hipMalloc(&m->ppre,
                    bm::pre_layout(n < bm::kSsmChunk ? n : bm::kSsmChunk, m->di, m->nh).total * 4));
-  m->pcap = n;
+  m->pcap = n;  // only once every buffer exists
   return 0;
 }
 

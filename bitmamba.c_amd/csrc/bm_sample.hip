@@ -50,8 +50,7 @@ constexpr int kHist = 256;
 constexpr int kFront = 64;          // blocks of the O(V) passes (one wave of partials)
 constexpr int kFrontThreads = 256;
 static_assert(kFront % (kThreads / 64) == 0, "whole pre-candidate lists per wave");
-// vocabularies up to 65535 entries: a segment is at most 4 * kFrontThreads
-static_assert((((65535 + kFront - 1) / kFront + 3) & ~3) <= 4 * kFrontThreads, "one row per block");
+constexpr int kMaxVocab = 256000;  // MAX_VOCAB of the loader (src/bitmamba.h:55)
 
 // vocabulary segment of each front block: a multiple of 4 entries
 __host__ __device__ __forceinline__ int front_seg(int V) { return ((V + kFront - 1) / kFront + 3) & ~3; }
@@ -91,6 +90,7 @@ constexpr int kCandLds = 512;      // candidates kept in LDS when they fit
 constexpr int kListsPerWave = kFront / (kThreads / 64);
 
 struct Smem {
+  unsigned radix[16 * kThreads];  // sort_large: per-thread digit counts, then offsets
   Cand stage[kStage];
   Cand cand[kCandLds];
   Cand sel[kPartial];
@@ -333,7 +333,7 @@ __device__ __forceinline__ uint32_t desc_key(float v) {
 // stable descending sort of n candidates in global memory (LSD radix, 4-bit
 // digits, each thread a contiguous run); the result ends in `a`
 __device__ void sort_large(Cand* a, Cand* b, int n, Smem& sm) {
-  unsigned short* cnt = (unsigned short*)sm.stage;  // [16][kThreads]
+  unsigned* cnt = sm.radix;  // [16][kThreads]
   const int per = (n + kThreads - 1) / kThreads;
   const int i0 = threadIdx.x * per, i1 = min(n, i0 + per);
   Cand* src = a;
@@ -344,7 +344,7 @@ __device__ void sort_large(Cand* a, Cand* b, int n, Smem& sm) {
     for (int d = 0; d < 16; ++d) c[d] = 0;
     for (int i = i0; i < i1; ++i) ++c[(desc_key(src[i].val) >> shift) & 15];
 #pragma unroll
-    for (int d = 0; d < 16; ++d) cnt[d * kThreads + threadIdx.x] = (unsigned short)c[d];
+    for (int d = 0; d < 16; ++d) cnt[d * kThreads + threadIdx.x] = c[d];
     __syncthreads();
     // exclusive offsets in (digit, thread) order: thread t scans its 16
     // entries t*16 .. t*16+15 of the flattened array, then the partials
@@ -352,13 +352,12 @@ __device__ void sort_large(Cand* a, Cand* b, int n, Smem& sm) {
     for (int e = 0; e < 16; ++e) part += cnt[threadIdx.x * 16 + e];
     unsigned total;
     unsigned base = block_scan(part, sm, &total);
-    unsigned short own[16];
+    unsigned own[16];
     for (int e = 0; e < 16; ++e) own[e] = cnt[threadIdx.x * 16 + e];
     __syncthreads();
-    // rewrite the counts as exclusive offsets (they fit: n <= 65535 is
-    // checked by the caller)
+    // rewrite the counts as exclusive offsets
     for (int e = 0; e < 16; ++e) {
-      cnt[threadIdx.x * 16 + e] = (unsigned short)base;
+      cnt[threadIdx.x * 16 + e] = base;
       base += own[e];
     }
     __syncthreads();
@@ -641,9 +640,12 @@ __global__ __launch_bounds__(kFrontThreads) void k_samp_hist(const float* __rest
   const uint64_t below = (1ull << lane) - 1ull;
   Cand* pre = sc.pre + (size_t)blockIdx.x * seg;
   int last = 0, off = 0;
-  {
-    const int i = i0 + 4 * (int)threadIdx.x;  // a segment is one row of float4s
-    const float v[4] = {q.x, q.y, q.z, q.w};
+  // the segment in rows of 4 * kFrontThreads entries (one row up to 65536
+  // vocabulary entries), each compacted in index order after the last
+  for (int i = i0 + 4 * (int)threadIdx.x, first = 1; i - 4 * (int)threadIdx.x < i1;
+       i += 4 * kFrontThreads, first = 0) {
+    const float4 qr = first ? q : load4(logits, i, i1);
+    const float v[4] = {qr.x, qr.y, qr.z, qr.w};
     bool h[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -873,7 +875,7 @@ hipError_t launch_sample(float* logits, int V, float temp, float min_p, float to
                          uint64_t* rng_state, void* scratch, const float* pmax, int npart,
                          int* ctl, int* hist, int* out_tokens, const float* embed, int dm,
                          float* x, hipStream_t s) {
-  if (V < 1 || V > 65535) return hipErrorInvalidValue;  // 16-bit radix offsets
+  if (V < 1 || V > kMaxVocab) return hipErrorInvalidValue;
   if ((uintptr_t)logits % 16) return hipErrorInvalidValue;  // float4 passes
   const SampleParams p{temp, min_p, top_p, top_k};
   const StepIO io{ctl, hist, out_tokens, embed, dm, x};
@@ -909,7 +911,7 @@ extern "C" int bm_hip_sample_advanced(float* logits, int vocab, float temp, floa
       bm::launch_sample(logits, vocab, temp, min_p, top_p, top_k, rng, workspace, nullptr, 0,
                         nullptr, nullptr, token_out, nullptr, 0, nullptr, (hipStream_t)stream);
   if (e != hipSuccess) {
-    bm_set_error("sample_advanced: %s (vocab %d, logits %p; vocab 1..65535, 16-byte aligned logits)",
+    bm_set_error("sample_advanced: %s (vocab %d, logits %p; vocab 1..256000, 16-byte aligned logits)",
                  hipGetErrorString(e), vocab, (void*)logits);
     return -1;
   }

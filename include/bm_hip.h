@@ -340,7 +340,7 @@ int bm_hip_model_set_sampler(bm_hip_model_t *m,
  * workspace: bm_hip_sample_workspace_bytes(vocab) bytes of device memory
  * (the reference's probs buffer, twice).  The token goes to token_out[0]
  * (device memory); enqueued on `stream`, no synchronization.  0, or -1 for
- * vocab outside 1..65535, misaligned logits or a null pointer. */
+ * vocab outside 1..256000, misaligned logits or a null pointer. */
 size_t bm_hip_sample_workspace_bytes(int vocab);
 int bm_hip_sample_advanced(float *logits,
                            int vocab,

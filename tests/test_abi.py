@@ -55,9 +55,10 @@ def test_synthetic_distributions():
     assert q.min() >= -127 and q.max() <= 127
 
 
-def test_bit2_rejects_garbage_via_set_mmap_free_parser():
-    # the product's BIT2 parser is only reachable through bm_hip_set_mmap on a
-    # GPU; here we check the image size formula against the writer
+def test_synth_image_size_matches_bit2_layout():
+    # the synthetic writer's image size against the BIT2 record layout
+    # (src/model.c:367-475: float records type, ndim, dims, data; ternary
+    # records type, rows, cols, scale, packed bytes)
     blob = bh.synth_model(1000, 128, 2, 4, 5)
     dm, di, nh, V = 128, 256, 4, 1000
     fl = lambda nd, n: 8 + 4 * nd + 4 * n

@@ -182,6 +182,73 @@ def test_wide_model_logits_vs_oracle(hip, d_model, n_heads, penalty):
         m.free()
 
 
+# Shapes the loader accepts that the fused decode kernels do not cover:
+# d_model % 64 != 0 (in_proj and LM head through the generic quantize +
+# product kernels), a head dim that is not a multiple of 16 (in_proj + the
+# per-head SSM kernel), d_inner > 8192 with head dims past 1024 (out_proj
+# through the generic kernels, several SSM blocks per head), and a vocabulary
+# past 65535 under the sampler.
+ODD_SHAPES = [  # (vocab, d_model, n_heads, penalty, sampler)
+    (300, 96, 4, 1.0, None),
+    (300, 96, 4, 1.3, None),
+    (257, 128, 32, 1.0, None),
+    (100, 4160, 5, 1.0, None),
+    (70001, 64, 2, 1.0, (0.9, 0.0, 0.95, 0)),
+    (70001, 64, 2, 1.2, (1.1, 0.05, 0.9, 40)),
+]
+
+
+@pytest.mark.parametrize("vocab,d_model,n_heads,penalty,sampler", ODD_SHAPES)
+def test_odd_shapes_vs_oracle(hip, vocab, d_model, n_heads, penalty, sampler):
+    """One-layer models of the shapes above: the prefill state, then every
+    step's logits (after the penalty; divided by the temperature when
+    sampled) and token bit-exact against the oracle (orc_sample for the
+    sampled ones), through single steps and through the captured graph of
+    bm_hip_model_generate."""
+    note("odd shape vocab=%d d_model=%d heads=%d penalty=%g sampler=%s"
+         % (vocab, d_model, n_heads, penalty, sampler))
+    blob = bh.synth_model(vocab, d_model, 1, n_heads, 5 + d_model + vocab, bh.SYNTH_UNIFORM)
+    prompt = bh.synth_prompt(5 + d_model, vocab, 8)
+    m = bh.Model(blob)
+    O, h = _oracle_model(blob)
+    try:
+        p = prompt[:-1].copy()
+        m.prefill(p)
+        O.orc_model_prefill(h, ptr(p), p.size)
+        cs, ss, pos = m.layer_state(0)
+        ocs = np.empty((3, m.d_inner), np.float32)
+        oss = np.empty(m.d_inner, np.float32)
+        assert pos == O.orc_model_layer_state(h, 0, ptr(ocs), ptr(oss))
+        same_bits(cs, ocs, "conv_state")
+        same_bits(ss, oss, "ssm_state")
+        rng = native.C.c_uint64(0x853c49e6748fea9b)
+        if sampler:
+            m.set_sampler(*sampler)
+            m.seed(0x853c49e6748fea9b)
+        hist, cur = [int(t) for t in prompt], int(prompt[-1])
+        for i in range(5):
+            harr = np.array(hist[-256:], np.int32)
+            t_dev = m.step(cur, harr, penalty)
+            t_orc = O.orc_model_step(h, cur, ptr(harr), harr.size, penalty)
+            lg = np.ctypeslib.as_array(O.orc_model_logits(h), (vocab,)).copy()
+            if sampler:
+                t_orc = O.orc_sample(ptr(lg), vocab, sampler[0], sampler[1], sampler[2],
+                                     sampler[3], native.C.byref(rng))
+            same_bits(m.logits(), lg, "logits step %d" % i)
+            assert t_dev == t_orc, i
+            hist.append(t_dev)
+            cur = t_dev
+        # the same steps as one captured graph each, from the prompt again
+        m.reset()
+        if sampler:
+            m.seed(0x853c49e6748fea9b)
+        toks, _ = m.generate(prompt, 5, penalty)
+        assert [int(t) for t in toks] == hist[len(prompt):]
+    finally:
+        O.orc_model_free(h)
+        m.free()
+
+
 # GEMM tiles of the 1B width: 300 tokens 64x128, 1220 in_proj 128x128, 2100
 # 128x256 (three SSM chunks); 255M width, 1030 tokens: in_proj 128x256,
 # out_proj 64x128, two SSM chunks

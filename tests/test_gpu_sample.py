@@ -3,8 +3,10 @@ against the oracle's restatement of sample_advanced (src/model.c:132-361).
 
 Bar: bit-exact token, scaled logits and generator state, over every branch
 of the sampler, vocabulary sizes that are not multiples of the kernel's
-4-wide loads (1, 3, 7, 4999, 50257) up to the 65535 limit, and logits with
-ties, infinities and a long tail far below the maximum.
+4-wide loads (1, 3, 7, 4999, 50257), vocabularies past 65535 (whose
+histogram pass walks several rows per block and whose full sort needs
+32-bit offsets) up to the loader's limit of 256000 (src/bitmamba.h:55),
+and logits with ties, infinities and a long tail far below the maximum.
 """
 import numpy as np
 import pytest
@@ -27,7 +29,7 @@ PARAMS = [
     (1.0, 1.0, 1.0, 0),        # only the maximum survives min_p
     (0.01, 0.0, 1.0, 0),       # greedy
 ]
-VOCABS = [1, 3, 7, 4999, 50257, 65535]
+VOCABS = [1, 3, 7, 4999, 50257, 65535, 65536, 100003, 256000]
 
 
 def _logits(kind, V, seed):
@@ -73,7 +75,7 @@ def test_sample_advanced_rejects(hip):
     buf = bh.DeviceBuffer(bh.lib().bm_hip_sample_workspace_bytes(65535) + 64)
     try:
         p = buf.ptr
-        for V in (0, -1, 65536):
+        for V in (0, -1, 256001):
             assert L.bm_hip_sample_advanced(p, V, 1.0, 0.0, 1.0, 0, p, p, p, None) == -1
         assert L.bm_hip_sample_advanced(p + 4, 8, 1.0, 0.0, 1.0, 0, p, p, p, None) == -1
         assert "aligned" in bh.last_error()
