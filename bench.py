@@ -17,8 +17,13 @@ Prints ONE JSON line.  Legs (all by default):
             of distinct weight rows in one launch, timed with HIP events on
             the library stream -> achieved GB/s vs 8 TB/s
   prefill   int8-MFMA GEMM at M=2048: 2048->8512 and 4096->2048, TOP/s
-  cpu       the reference's own AVX2 build (oracle/_ref) on the host cores:
-            a bounded sample of the same decode workload
+  cpu       the reference's own AVX2 build (oracle/_ref) on the host cores,
+            at every thread the box grants (at most 16) and at one thread,
+            in a child process before the GPU starts: bounded samples of the
+            1B and 255M decodes, the 1024-token 1B prefill, the two M=2048
+            prefill products (bitlinear_forward_batch) and the K = N = 8192
+            int8 products at M = 1, 16 and 4096 (the row kernel per token);
+            each GPU sub-object carries its CPU figures under "cpu"
   gemv1     the single K=1024 -> N=4384 BitLinear (uniform ternary, N(0,1)
             input): device call time (warm, cache-resident), the host-pointer
             drop-in call (PCIe included), and the reference's own CPU build
@@ -439,83 +444,218 @@ def cpu_threads():
     return max(1, min(allowed, 16))
 
 
-def cpu_child(threads, sample_tokens, budget_s):
+def _ref_model_file(c, d):
+    """The synthetic image of config c written to a file in d (the reference
+    loads models from files, src/model.c:499-540)."""
+    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
+                          c["dist"])
+    path = os.path.join(d, "model_%d.bin" % c["d_model"])
+    blob.tofile(path)
+    return path
+
+
+def _cpu_decode(R, native, path, c, max_steps, budget_s, what):
+    """Greedy decode tok/s of the reference (src/main.c:443-500 pattern):
+    prefill of the prompt but its last token, then steps until max_steps
+    or the time budget."""
+    h = R.bmref_model_load(path.encode())
+    if not h:
+        raise RuntimeError("reference model_load failed")
+    beat("cpu: %s model loaded" % what)
+    prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
+    p = np.ascontiguousarray(prompt[:-1], np.int32)
+    R.bmref_model_prefill(h, native.ptr(p), p.size)
+    beat("cpu: %s prompt prefilled" % what)
+    hist, cur = [int(t) for t in prompt], int(prompt[-1])
+    times = []
+    start = time.perf_counter()
+    for i in range(max_steps):
+        harr = np.array(hist[-256:], np.int32)
+        t0 = time.perf_counter()
+        cur = R.bmref_model_step(h, cur, native.ptr(harr), harr.size, 1.0)
+        times.append(time.perf_counter() - t0)
+        hist.append(cur)
+        if i % 16 == 0:
+            beat("cpu: %s step %d %.2f ms" % (what, i, times[-1] * 1e3))
+        if time.perf_counter() - start > budget_s:
+            break
+    R.bmref_model_free(h)
+    return dict(value=round(len(times) / sum(times), 2), unit="tok/s", steps=len(times))
+
+
+def _cpu_prefill(R, native, path, c, n_tokens, budget_s):
+    """model_prefill (src/model.c:1045-1153) of n_tokens: tokens/s."""
+    h = R.bmref_model_load(path.encode())
+    toks = np.ascontiguousarray(bh.synth_prompt(c["seed"] + 1, c["vocab"], n_tokens), np.int32)
+    t0 = time.perf_counter()
+    R.bmref_model_prefill(h, native.ptr(toks), toks.size)
+    dt = time.perf_counter() - t0
+    R.bmref_model_free(h)
+    return dict(tokens=n_tokens, ms=round(dt * 1e3, 1), tok_s=round(n_tokens / dt, 1))
+
+
+def _cpu_batch_gemm(R, native, K, N, M):
+    """bitlinear_forward_batch (AVX2: src/arch/avx2.c:384-452, with the
+    per-token RMSNorm + int8 quantization of each token) on the prefill
+    GEMM's inputs, M tokens: TOP/s of the 2*M*N*K products."""
+    w = bh.synth_ternary(11, 1, N, K, bh.SYNTH_UNIFORM)
+    x = bh.synth_normal(11, 2, (M, K), 1.0)
+    g = np.ones(K, np.float32)
+    out = np.empty((M, N), np.float32)
+    xn = np.empty(K, np.float32)
+    xq = np.zeros((M, K + 32), np.int8)
+    args = (native.ptr(x), M, K, native.ptr(w), N, K, C.c_float(0.02), native.ptr(g),
+            native.ptr(out), native.ptr(xn), native.ptr(xq), K + 32)
+    R.bmref_bitlinear_forward_batch(*args)  # warm-up
+    t0 = time.perf_counter()
+    R.bmref_bitlinear_forward_batch(*args)
+    dt = time.perf_counter() - t0
+    return dict(tokens=M, ms=round(dt * 1e3, 2), tops=round(2.0 * M * N * K / dt / 1e12, 4))
+
+
+def _cpu_rows_int8(R, native, w, K, N, xq):
+    """The reference's row kernel (the AVX2 row worker, src/arch/avx2.c:
+    99-268) on int8 activations, one call per token: seconds per token."""
+    out = np.empty(N, np.float32)
+    t = []
+    for m in range(xq.shape[0]):
+        row = np.ascontiguousarray(xq[m])
+        t0 = time.perf_counter()
+        R.bmref_rows_int8(native.ptr(row), native.ptr(w), N, K, C.c_float(1.0), native.ptr(out))
+        t.append(time.perf_counter() - t0)
+    return t
+
+
+def beat(msg):
+    """A progress line of a CPU child (read by its parent's watchdog)."""
+    print("P " + msg, flush=True)
+    log(msg)
+
+
+def cpu_child(threads, budget_s):
     """Runs in a separate process that never touches the GPU: the
     reference's own C (oracle/_ref: dispatch_init -> AVX2+FMA kernels, its
-    thread pool with the default spin wait) decoding the same synthetic
-    1B-shape model.  Prints one JSON line."""
+    thread pool with the default spin wait) on bounded samples of every
+    workload of the bench.  Prints one JSON line per leg ("CPU <leg> ...")
+    so that a leg that runs out of time loses only itself."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import native
     R = native.ref()
     name = R.bmref_init(threads, 1).decode()
     R.bmref_set_poll(100)
-    c = CFG_1B
-    blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
-                          c["dist"])
-    prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
-    d = tempfile.gettempdir()
-    with tempfile.NamedTemporaryFile(suffix=".bin", dir=d) as f:
-        blob.tofile(f.name)
-        del blob
-        log("cpu: model file written, loading with %d threads (%s kernels)" % (threads, name))
-        h = R.bmref_model_load(f.name.encode())
-        log("cpu: model loaded")
-        p = np.ascontiguousarray(prompt[:-1], np.int32)
-        t0 = time.perf_counter()
-        R.bmref_model_prefill(h, native.ptr(p), p.size)
-        log("cpu: prefill of %d tokens %.2fs" % (p.size, time.perf_counter() - t0))
-        hist = [int(t) for t in prompt]
-        cur = int(prompt[-1])
-        times = []
-        start = time.perf_counter()
-        for i in range(sample_tokens):
-            harr = np.array(hist[-256:], np.int32)
-            t0 = time.perf_counter()
-            cur = R.bmref_model_step(h, cur, native.ptr(harr), harr.size, 1.0)
-            times.append(time.perf_counter() - t0)
-            hist.append(cur)
-            if i % 8 == 0:
-                log("cpu: step %d %.1f ms" % (i, times[-1] * 1e3))
-            if time.perf_counter() - start > budget_s:
-                break
-        R.bmref_model_free(h)
+    one = threads == 1
+
+    def emit(leg, d):
+        d.update(threads=threads, kernels=name)
+        print("CPU %s %s" % (leg, json.dumps(d)), flush=True)
+
+    with tempfile.TemporaryDirectory(dir=tempfile.gettempdir()) as d:
+        p1b = _ref_model_file(CFG_1B, d)
+        beat("cpu[%d]: 1B model file written" % threads)
+        emit("decode_1b", _cpu_decode(R, native, p1b, CFG_1B, 64, budget_s, "1B"))
+        # time to first token: 1024 tokens (a 256-token sample on one thread)
+        n_pf = 256 if one else 1024
+        r = _cpu_prefill(R, native, p1b, CFG_1B, n_pf, budget_s)
+        r["sample"] = "%d-token prefill" % n_pf
+        emit("prefill_1b", r)
+        beat("cpu[%d]: prefill %s" % (threads, json.dumps(r)))
+        os.unlink(p1b)
+        p255 = _ref_model_file(CFG_255M, d)
+        emit("decode_255m", _cpu_decode(R, native, p255, CFG_255M, 64 if one else 128, budget_s,
+                                        "255M"))
+        os.unlink(p255)
+    # prefill GEMM shapes at M=2048 (512 tokens on one thread)
+    for K, N in ((2048, 8512), (4096, 2048)):
+        M = 512 if one else 2048
+        r = _cpu_batch_gemm(R, native, K, N, M)
+        r["sample"] = "%d of the 2048 tokens" % M if one else "all 2048 tokens"
+        emit("gemm_%dx%dx%d" % (2048, K, N), r)
+        beat("cpu[%d]: gemm K=%d N=%d %s" % (threads, K, N, json.dumps(r)))
+    # stress shape K = N = 8192, int8 activations: M = 1, 16 and a sample of
+    # the 4096-token product (the reference has no int8 batch entry: one row
+    # kernel call per token)
+    K = N = 8192
+    w = bh.synth_ternary(5, 1, N, K, bh.SYNTH_P0_60)
+    xq = bh.synth_int8(5, 2, (16, K))
+    beat("cpu[%d]: stress shape" % threads)
+    _cpu_rows_int8(R, native, w, K, N, xq[:2])  # warm-up
+    t1 = _cpu_rows_int8(R, native, w, K, N, xq[:1] if one else xq[:1].repeat(9, 0))
+    t16 = _cpu_rows_int8(R, native, w, K, N, xq)
+    us1 = float(np.median(t1)) * 1e6
+    us16 = float(sum(t16)) * 1e6
+    samp = 16 if one else 64
+    xs = bh.synth_int8(5, 3, (samp, K))
+    ts = _cpu_rows_int8(R, native, w, K, N, xs)
+    per_tok = float(sum(ts)) / samp
+    emit("stress", dict(M1_us=round(us1, 1), M1_weight_GBps=round(N * K / 4 / us1 / 1e3, 2),
+                        M16_us=round(us16, 1), M16_tops=round(2.0 * 16 * N * K / us16 / 1e6, 4),
+                        M4096_est_ms=round(per_tok * 4096 * 1e3, 1),
+                        M4096_tops=round(2.0 * N * K / per_tok / 1e12, 4),
+                        sample="M=4096 from %d of its tokens, one row-kernel call each" % samp))
     R.bmref_shutdown()
-    tok_s = len(times) / sum(times)
-    print(json.dumps(dict(value=round(tok_s, 2), unit="tok/s", cores=threads, kind="reference",
-                          sample="%d greedy steps of the same 1B-shape decode after a 7-token "
-                                 "prefill (reference kernels: %s, %d threads, spin-wait pool)"
-                                 % (len(times), name, threads))), flush=True)
 
 
-def leg_cpu(sample_tokens=64, budget_s=25.0, timeout_s=100):
-    """The CPU baseline, in a child process; bounded so that the bench line
-    always comes out: a child that overruns is killed and tried once more
-    with half the threads (a spin-wait pool can stall when the box's CPU
-    share is oversubscribed)."""
+def run_cpu_suite(threads, stall_s=45.0, total_s=240.0):
+    """The CPU baseline legs in a child process, watched: a child that
+    prints nothing for stall_s is killed and run again (same thread count
+    once, then half), so that the bench line always comes out; the result
+    records the retries (`retried`) and where a killed child had got to.
+    The reference's pool spins without yielding in its completion waits and
+    barriers (src/threadpool.c:515-521, 594-609), so one descheduled thread
+    holds up all the others."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import native
     import subprocess
+    import threading
     if not native.ref_available():
-        return None
-    threads = cpu_threads()
-    for attempt in range(2):
-        cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child", str(threads),
-               str(sample_tokens), str(budget_s)]
-        try:
-            r = subprocess.run(cmd, stdout=subprocess.PIPE, timeout=timeout_s, text=True)
-        except subprocess.TimeoutExpired:
-            log("cpu: baseline child with %d threads exceeded %ds" % (threads, timeout_s))
-            threads = max(1, threads // 2)
-            continue
-        lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
-        return json.loads(lines[-1]) if r.returncode == 0 and lines else None
-    log("cpu: no baseline reported")
-    return None
+        return {}
+    out, stalls = {}, []
+    start = time.time()
+    for t in (threads, threads, max(1, threads // 2))[:3 if threads > 1 else 2]:
+        cmd = [sys.executable, os.path.abspath(__file__), "--cpu-child", str(t), "25"]
+        proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, text=True, bufsize=1)
+        lines, last = [], [time.time()]
+
+        def read(f=proc.stdout, lines=lines, last=last):
+            for l in f:
+                lines.append(l)
+                last[0] = time.time()
+
+        rd = threading.Thread(target=read, daemon=True)
+        rd.start()
+        killed = False
+        while proc.poll() is None:
+            time.sleep(0.2)
+            if time.time() - last[0] > stall_s or time.time() - start > total_s:
+                proc.kill()
+                killed = True
+                proc.wait()
+        rd.join(5)
+        got = 0
+        for l in lines:
+            if l.startswith("CPU "):
+                _, leg, js = l.split(" ", 2)
+                d = json.loads(js)
+                d["retried"] = bool(stalls)
+                out[leg] = d
+                got += 1
+        if not killed and proc.returncode == 0 and "stress" in out:
+            break
+        where = [l[2:].strip() for l in lines if l.startswith("P ")]
+        stalls.append(dict(threads=t, after=where[-1] if where else "start"))
+        log("cpu: child with %d threads stopped (%s) after: %s"
+            % (t, "no output for %ds" % stall_s if killed else "rc %s" % proc.returncode,
+               stalls[-1]["after"]))
+        if time.time() - start > total_s:
+            break
+    if stalls:
+        out["stalls"] = stalls
+    return out
 
 
 def main():
-    if len(sys.argv) == 5 and sys.argv[1] == "--cpu-child":
-        cpu_child(int(sys.argv[2]), int(sys.argv[3]), float(sys.argv[4]))
+    if len(sys.argv) == 4 and sys.argv[1] == "--cpu-child":
+        cpu_child(int(sys.argv[2]), float(sys.argv[3]))
         return
     if len(sys.argv) == 4 and sys.argv[1] == "--cpu-gemv":
         cpu_gemv_child(int(sys.argv[2]), int(sys.argv[3]))
@@ -532,10 +672,24 @@ def main():
               "multi-GPU path at bs=1); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     legs = set(a.legs.split(","))
-    # the CPU baseline first, while this process has not started the GPU
-    # runtime (its child never touches the GPU)
-    cpu = leg_cpu() if "cpu" in legs else None
-    if cpu:
+    # the CPU baselines first, while this process has not started the GPU
+    # runtime (the children never touch the GPU): all host threads the box
+    # grants (at most 16), then one thread
+    cpu_n = run_cpu_suite(cpu_threads()) if "cpu" in legs else {}
+    cpu_1 = run_cpu_suite(1) if "cpu" in legs else {}
+    cpu_stalls = cpu_n.pop("stalls", []) + cpu_1.pop("stalls", [])
+    cpu = None
+    if "decode_1b" in cpu_n:
+        d = cpu_n["decode_1b"]
+        cpu = dict(value=d["value"], unit="tok/s", cores=d["threads"], threads=d["threads"],
+                   retried=d["retried"], kind="reference",
+                   sample="%d greedy steps of the same 1B-shape decode after a 7-token prefill "
+                          "(reference kernels: %s, %d threads, spin-wait pool)"
+                          % (d["steps"], d["kernels"], d["threads"]))
+        if "decode_1b" in cpu_1:
+            cpu["value_1_thread"] = cpu_1["decode_1b"]["value"]
+        if cpu_stalls:
+            cpu["stalled_children"] = cpu_stalls
         log("cpu baseline: %s" % json.dumps(cpu))
     L = bh.lib()
     if not L.bm_hip_init():
@@ -594,6 +748,20 @@ def main():
                     tokens_match_reference=match)
     else:
         line.update(value=None, ms_per_step=None)
+    # the reference's CPU figures beside each GPU figure
+    def cpu_of(leg):
+        return {"threads_%d" % r[leg]["threads"]: r[leg] for r in (cpu_n, cpu_1) if leg in r}
+    if cpu_n or cpu_1:
+        line["cpu_decode_1b"] = cpu_of("decode_1b")
+        if res.get("prefill_model") is not None:
+            res["prefill_model"]["cpu"] = cpu_of("prefill_1b")
+        if d255:
+            d255["cpu"] = cpu_of("decode_255m")
+        if pre:
+            for k in pre:
+                pre[k]["cpu"] = cpu_of("gemm_" + k)
+        if strs:
+            strs["cpu"] = cpu_of("stress")
     line["decode_sampled"] = res.get("sampled")
     line["prefill_1b"] = res.get("prefill_model")
     line["roofline"] = roof
