@@ -72,6 +72,18 @@ hipError_t launch_rms_norm(const float *x, int n, const float *gamma,
                            float *out, float *max_out, hipStream_t s);
 hipError_t launch_canonicalize(uint8_t *p, size_t bytes, hipStream_t s);
 
+// One BitLinear call (RMSNorm + int8 + GEMV, canonical weights) on mapped
+// host memory in a single launch of dropin_blocks(N, K) blocks
+// (bm_decode.hip): x, out, and the copies xn (normalized input) and xq
+// (int8 input) are mapped host buffers; block b writes seq to the
+// host-mapped word flags[b] once its results are visible to the host.
+// Needs rows_fit(K).
+bool rows_fit(int K);
+int dropin_blocks(int N, int K);
+hipError_t launch_dropin(const float *x, int K, const float *gamma, const uint8_t *W, int N,
+                         float w_scale, float *out, float *xn, int8_t *xq, unsigned *flags,
+                         unsigned seq, hipStream_t s);
+
 // MFMA tile layout of packed weights (bm_gemm.hip): [ceil(N/32)][K/128]
 // blocks of 1 KB, each the 32 packed bytes of one 128-column stage of 32
 // consecutive rows, row after row; code 11 rewritten to 10.  K % 128 == 0.

@@ -171,15 +171,18 @@ __device__ __forceinline__ uint32_t q8_of(float v, float scale_x) {
 // split-nibble layout + slice sums; returns scale_x.
 template <int C>
 __device__ float pro_quant(const float4 (&xv)[C], const float4 (&gv)[C], float rms, int K,
-                           const Lds& l) {
+                           const Lds& l, float* __restrict__ xn_out = nullptr,
+                           int8_t* __restrict__ xq_out = nullptr) {
   const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, n4 = K >> 2;
   float4 v[C];
   float mx = 0.0f;
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     v[i] = scale4(xv[i], rms, gv[i]);
-    if (tid + i * nt < n4)
+    if (tid + i * nt < n4) {
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+      if (xn_out) ((float4*)xn_out)[tid + i * nt] = v[i];
+    }
   }
   mx = wave_max_f32(mx);
   if (lane == 0) l.bc[8 + wave] = mx;
@@ -190,9 +193,12 @@ __device__ float pro_quant(const float4 (&xv)[C], const float4 (&gv)[C], float r
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     const int c = tid + i * nt;
-    if (c < n4)
-      ((uint32_t*)l.q8)[c] = q8_of(v[i].x, scale_x) | (q8_of(v[i].y, scale_x) << 8) |
-                             (q8_of(v[i].z, scale_x) << 16) | (q8_of(v[i].w, scale_x) << 24);
+    if (c < n4) {
+      const uint32_t q4 = q8_of(v[i].x, scale_x) | (q8_of(v[i].y, scale_x) << 8) |
+                          (q8_of(v[i].z, scale_x) << 16) | (q8_of(v[i].w, scale_x) << 24);
+      ((uint32_t*)l.q8)[c] = q4;
+      if (xq_out) ((uint32_t*)xq_out)[c] = q4;
+    }
   }
   __syncthreads();
   // 16 columns per thread from one 16-byte LDS read -> split nibbles
@@ -276,20 +282,39 @@ __device__ __forceinline__ float chain_rms(const Lds& l) {
   return l.bc[0];
 }
 
+// the thread's 16-column group of the input and of the norm weights, loaded
+// at kernel entry (before the weight rows, so that the prologue's first
+// wait covers these loads only)
+template <bool PRENORM>
+struct SplitIn {
+  float4 xv[4], gv[4], gp[PRENORM ? 4 : 1];
+};
+
 template <int G, bool PRENORM>
-__device__ float split_prologue(const float* __restrict__ x, const float* __restrict__ g_pre,
-                                const float* __restrict__ g, const Lds& l) {
+__device__ __forceinline__ void split_load(SplitIn<PRENORM>& in, const float* __restrict__ x,
+                                           const float* __restrict__ g_pre,
+                                           const float* __restrict__ g) {
+  constexpr int NG = 1024 * G / 16;
+  const int c4 = 4 * ((int)threadIdx.x < NG ? (int)threadIdx.x : 0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    in.xv[k] = ((const float4*)x)[c4 + k];
+    in.gv[k] = ((const float4*)g)[c4 + k];
+    if constexpr (PRENORM) in.gp[k] = ((const float4*)g_pre)[c4 + k];
+  }
+}
+
+template <int G, bool PRENORM>
+__device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l,
+                                float* __restrict__ xn_out = nullptr,
+                                int8_t* __restrict__ xq_out = nullptr) {
   constexpr int NG = 1024 * G / 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool has = tid < NG;
   const int c4 = 4 * (has ? tid : 0);
-  float4 xv[4], gv[4], gp[PRENORM ? 4 : 1];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    xv[k] = ((const float4*)x)[c4 + k];
-    gv[k] = ((const float4*)g)[c4 + k];
-    if constexpr (PRENORM) gp[k] = ((const float4*)g_pre)[c4 + k];
-  }
+  float4 (&xv)[4] = in.xv;
+  const float4 (&gv)[4] = in.gv;
+  const float4 (&gp)[PRENORM ? 4 : 1] = in.gp;
   put_squares<G>(xv, has, l);
   float rms = chain_rms<G>(l);
   if constexpr (PRENORM) {
@@ -306,6 +331,7 @@ __device__ float split_prologue(const float* __restrict__ x, const float* __rest
     xv[k] = scale4(xv[k], rms, gv[k]);
     mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[k].x), fabsf(xv[k].y)),
                          fmaxf(fabsf(xv[k].z), fabsf(xv[k].w))));
+    if (xn_out && has) ((float4*)xn_out)[c4 + k] = xv[k];
   }
   mx = wave_max_f32(has ? mx : 0.0f);
   if (lane == 0) l.bc[8 + wave] = mx;
@@ -333,6 +359,14 @@ __device__ float split_prologue(const float* __restrict__ x, const float* __rest
       ho |= (uint32_t)((q[2 * n + 1] >> 4) & 15) << (4 * n);
     }
     *(uint4*)(l.nib + 4 * tid) = make_uint4(le, lo, he, ho);
+    if (xq_out) {
+      uint32_t b[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        b[k] = (uint32_t)(q[4 * k] & 255) | (uint32_t)(q[4 * k + 1] & 255) << 8 |
+               (uint32_t)(q[4 * k + 2] & 255) << 16 | (uint32_t)(q[4 * k + 3] & 255) << 24;
+      *(uint4*)(xq_out + 16 * tid) = make_uint4(b[0], b[1], b[2], b[3]);
+    }
   }
   const int ssum = wave_sum_i32(qsum);  // the wave's 64 groups = slice `wave`
   if (lane == 0 && wave < G) l.slices[wave] = ssum;
@@ -393,15 +427,31 @@ __device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32
 //            2: the rows are stored multiplied by 1/temp (the sampler's
 //               temperature, src/model.c:160-166) and each block writes the
 //               max of what it stored under `x > m` from -1e30f
+//   DROP:    a single call on mapped host memory (x in, out, and block 0's
+//            copies of the normalized and int8 input out): each block
+//            stages its rows in LDS, writes them as one contiguous run and
+//            then writes dr.seq to its own host-mapped word dr.flags[block],
+//            which the caller polls instead of synchronizing the stream (no
+//            device-wide counter: atomics on one word serialize across the
+//            XCDs, ~70 ns per block)
 // ---------------------------------------------------------------------------
-template <int T, int P, int NPF, int C, bool PRENORM, int MODE, int PICK, bool WP>
+struct DropOut {
+  float* xn;        // normalized input, written by block 0 (or null)
+  int8_t* xq;       // int8 input, written by block 0 (or null)
+  unsigned* flags;  // host-mapped completion words, one per block
+  unsigned seq;
+};
+
+template <int T, int P, int NPF, int C, bool PRENORM, int MODE, int PICK, bool WP,
+          bool DROP = false>
 __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma_pre,
                                                     const float* __restrict__ gamma,
                                                     const uint8_t* __restrict__ W, int N,
                                                     float w_scale, float* __restrict__ out,
                                                     float* __restrict__ part_v,
-                                                    int* __restrict__ part_i, float temp) {
+                                                    int* __restrict__ part_i, float temp,
+                                                    DropOut dr) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int RPW = 64 / T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -415,7 +465,10 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
 
   // the input vectors first (the prologue waits for them), then the weights
   float4 sx[WP ? 1 : C], sg[WP ? 1 : C], sg2[PRENORM && !WP ? C : 1];
-  if constexpr (!WP) {
+  SplitIn<PRENORM> sin;
+  if constexpr (WP) {
+    split_load<C, PRENORM>(sin, x, gamma_pre, gamma);
+  } else {
     stage_load<C>(sx, x, K);
     stage_load<C>(sg, PRENORM ? gamma_pre : gamma, K);
     if constexpr (PRENORM) stage_load<C>(sg2, gamma, K);
@@ -445,9 +498,11 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   }
 
   const Lds l = lds_carve(lds, K);
+  float* const xn_out = DROP && b == 0 ? dr.xn : nullptr;
+  int8_t* const xq_out = DROP && b == 0 ? dr.xq : nullptr;
   float scale_x;
   if constexpr (WP) {
-    scale_x = split_prologue<C, PRENORM>(x, gamma_pre, gamma, l);
+    scale_x = split_prologue<C, PRENORM>(sin, l, xn_out, xq_out);
   } else {
     float rms = pro_rms<C>(sx, K, l);
     if constexpr (PRENORM) {
@@ -455,9 +510,9 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
 #pragma unroll
       for (int i = 0; i < C; ++i) sx[i] = scale4(sx[i], rms, sg[i]);
       rms = pro_rms<C>(sx, K, l);
-      scale_x = pro_quant<C>(sx, sg2, rms, K, l);
+      scale_x = pro_quant<C>(sx, sg2, rms, K, l, xn_out, xq_out);
     } else {
-      scale_x = pro_quant<C>(sx, sg, rms, K, l);
+      scale_x = pro_quant<C>(sx, sg, rms, K, l, xn_out, xq_out);
     }
   }
   const float inv = inv_scale_of(scale_x, w_scale);
@@ -468,10 +523,15 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   float best_v = PICK == 2 ? -1e30f : -1e9f;
   int best_i = 0x7fffffff;
   const float inv_temp = PICK == 2 ? cr_divf(1.0f, temp) : 1.0f;
+  // DROP: the block's rows [r0, r0 + rows) go to LDS first (the squares'
+  // area, free after the prologue; a block owns at most 4 * NPF * RPW rows)
+  const int r0 = g0 * RPW;
   auto emit = [&](int r, float o, float res) {
     if (u == 0 && r < N) {
       if (PICK == 2) o = __fmul_rn(o, inv_temp);
-      if (MODE == 1)
+      if (DROP)
+        l.sq[r - r0] = o;
+      else if (MODE == 1)
         out[r] = __fadd_rn(res, o);
       else
         out[r] = o;
@@ -503,6 +563,19 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       o = row_finish<T>(dot64(w, xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
     }
     emit(r, o, MODE == 1 && u == 0 && r < N ? out[r] : 0.0f);
+  }
+
+  if constexpr (DROP) {
+    __syncthreads();
+    const int r_end = min(g1 * RPW, N);
+    for (int r = r0 + tid; r < r_end; r += blockDim.x) out[r] = l.sq[r - r0];
+    __syncthreads();
+    if (tid == 0) {
+      // the block's stores (and block 0's copies) reach the host before
+      // its completion word does
+      __threadfence_system();
+      __hip_atomic_store(dr.flags + b, dr.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 
   if constexpr (PICK == 2) {
@@ -594,8 +667,14 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
     return base + 2 * hd + (r - 2 * kCB);
   };
 
+  // the ring position first (nothing waits for it until the SSM step), the
+  // input vector next (the prologue waits for it), then the weights
+  const int pos = a.ctl[CTL_POS];
   float4 sx[WP ? 1 : C], sg[WP ? 1 : C];
-  if constexpr (!WP) {
+  SplitIn<false> sin;
+  if constexpr (WP) {
+    split_load<C, false>(sin, x, nullptr, gamma);
+  } else {
     stage_load<C>(sx, x, K);
     stage_load<C>(sg, gamma, K);
   }
@@ -614,15 +693,11 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   }
 
   // SSM inputs of this thread's channel (threads 0..kCB-1), fetched while the
-  // prologue runs
+  // prologue runs: all three ring slots, so that no address waits for pos
   const int c = tid < kCB ? tid : 0;
   const int idx = h * hd + q * kCB + c;
-  const int pos = a.ctl[CTL_POS];
-  const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
-  const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
-  const float tap0 = a.cs[(size_t)pos * a.di + idx];
-  const float tap1 = a.cs[(size_t)t1 * a.di + idx];
-  const float tap2 = a.cs[(size_t)t2 * a.di + idx];
+  const float ring0 = a.cs[idx], ring1 = a.cs[(size_t)a.di + idx];
+  const float ring2 = a.cs[2 * (size_t)a.di + idx];
   const float cw0 = a.cw[idx], cw1 = a.cw[a.di + idx], cw2 = a.cw[2 * a.di + idx];
   const float cw3 = a.cw[3 * a.di + idx], cbias = a.cb[idx], st0 = a.ssm[idx], Dc = a.D[idx];
   const float dtb = a.dt_bias[h], Ah = a.A[h];
@@ -630,7 +705,7 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   const Lds l = lds_carve(lds, K);
   float scale_x;
   if constexpr (WP) {
-    scale_x = split_prologue<C, false>(x, nullptr, gamma, l);
+    scale_x = split_prologue<C, false>(sin, l);
   } else {
     const float rms = pro_rms<C>(sx, K, l);
     scale_x = pro_quant<C>(sx, sg, rms, K, l);
@@ -660,6 +735,10 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   // head's softplus and decay; then wave 0 forms the state and y
   __shared__ float s_tail[2 * kCB + 2];
   if (wave == 0 && lane < kCB) {
+    // taps in age order from the ring position (src/block.c:107)
+    const float tap0 = pos == 0 ? ring0 : (pos == 1 ? ring1 : ring2);
+    const float tap1 = pos == 0 ? ring1 : (pos == 1 ? ring2 : ring0);
+    const float tap2 = pos == 0 ? ring2 : (pos == 1 ? ring0 : ring1);
     const float xin = s_proj[kCB + c];
     float conv = __fadd_rn(cbias, __fmul_rn(tap0, cw0));
     conv = __fadd_rn(conv, __fmul_rn(tap1, cw1));
@@ -797,34 +876,34 @@ static int rows_blocks(int N, int K) {
   return b < 1 ? 1 : b;
 }
 
-template <int NPF, bool PRENORM, int MODE, int PICK>
+template <int NPF, bool PRENORM, int MODE, int PICK, bool DROP = false>
 static hipError_t rows_t(const float* x, int K, const float* gpre, const float* g,
                          const uint8_t* W, int N, float w_scale, float* out, float* pv, int* pi,
-                         hipStream_t s, float temp = 1.0f) {
+                         hipStream_t s, float temp = 1.0f, DropOut dr = DropOut{}) {
   const size_t lds = lds_bytes(K);
   const dim3 grid(rows_blocks<NPF>(N, K)), block(256);
   if (K % 64 != 0) return hipErrorInvalidValue;
   if (K == 1024)
-    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else if (K == 2048)
-    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else if (K == 4096)
-    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, true>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else if (K <= 1024)
-    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, false, DROP>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else if (K <= 2048)
-    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, false, DROP>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else if (K <= 4096)
-    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, false, DROP>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else if (K <= 8192)
-    hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK, false>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp);
+    hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK, false, DROP>), grid, block,
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -847,6 +926,16 @@ bool inproj_ssm_fits(int K, int hd) { return K % 64 == 0 && K <= 8192 && hd % kC
 
 // the shapes the fused row kernels (in_proj, out_proj, LM head) cover
 bool rows_fit(int K) { return K % 64 == 0 && K <= 8192; }
+
+int dropin_blocks(int N, int K) { return rows_blocks<4>(N, K); }
+
+hipError_t launch_dropin(const float* x, int K, const float* gamma, const uint8_t* W, int N,
+                         float w_scale, float* out, float* xn, int8_t* xq, unsigned* flags,
+                         unsigned seq, hipStream_t s) {
+  if (!rows_fit(K) || N < 1) return hipErrorInvalidValue;
+  return rows_t<4, false, 0, 0, true>(x, K, nullptr, gamma, W, N, w_scale, out, nullptr, nullptr,
+                                      s, 1.0f, DropOut{xn, xq, flags, seq});
+}
 
 // in_proj + SSM for every head: y (and the states) updated in one launch
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,

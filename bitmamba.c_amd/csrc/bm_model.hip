@@ -347,7 +347,6 @@ hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
                           float w_scale, float* x, hipStream_t s);
 bool inproj_ssm_fits(int K, int hd);
-bool rows_fit(int K);
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
                              const float* cw, const float* cb, float* cs, float* ssm,

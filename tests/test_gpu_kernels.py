@@ -321,6 +321,84 @@ def test_dropin_reused_host_buffers(hip):
         same_bits(out, ref, "out seed %d" % seed)
 
 
+# images registered with bm_hip_set_mmap stay registered for the process:
+# they are kept alive here so that no later array reuses their addresses
+_REGISTERED = []
+
+
+def _dropin_call(hip, x, w, nw, N, K):
+    out = np.full(N, np.nan, np.float32)
+    xn = np.full(K, np.nan, np.float32)
+    xq = np.full(K + 32, 77, np.int8)
+    hip.hip_bitlinear_forward(ptr(x), K, C.byref(w), C.byref(nw), ptr(out), ptr(xn), ptr(xq))
+    return out, xn, xq
+
+
+def _dropin_ref(x, packed, N, K, scale, g):
+    O = native.oracle()
+    ref = np.empty(N, np.float32)
+    rxn = np.empty(K, np.float32)
+    rxq = np.zeros(K + 32, np.int8)
+    O.orc_bitlinear_forward(ptr(x), K, ptr(packed), N, K, C.c_float(scale), ptr(g), ptr(ref),
+                            ptr(rxn), ptr(rxq))
+    return ref, rxn, rxq
+
+
+# one token: the single-launch path (K % 64 == 0, outputs within the mapped
+# buffer, at most 320 blocks) and the two-launch path (K = 1000, the
+# 50257-row products, and an output too large for the mapped buffer); calls
+# alternate shapes so that each one must see its own completion words
+DROPIN_SHAPES = [(64, 1), (128, 3), (1024, 4192), (1000, 77), (1536, 65), (2048, 8384),
+                 (3072, 130), (4096, 2048), (8192, 300), (2048, 50257), (1024, 70000),
+                 (64, 2), (1024, 4384)]
+
+
+def test_dropin_single_token_shapes(hip):
+    """hip_bitlinear_forward at one token, out / x_norm / x_quant bit-exact
+    against the oracle's bitlinear_forward (src/kernel.c:388-447) for each
+    shape, on weights uploaded per call (codes 11 included)."""
+    for i, (K, N) in enumerate(DROPIN_SHAPES):
+        note("drop-in one token K=%d N=%d" % (K, N))
+        r = rnd(400 + i)
+        packed = r.integers(0, 256, (N, (K + 3) // 4), dtype=np.uint8)
+        g = (1.0 + 0.1 * r.standard_normal(K)).astype(np.float32)
+        x = r.standard_normal(K).astype(np.float32)
+        x[r.integers(0, K, 2)] *= 8.0
+        w = bh.make_tensor(packed, N, K, 0.025)
+        nw = bh.make_tensor(data=g)
+        out, xn, xq = _dropin_call(hip, x, w, nw, N, K)
+        ref, rxn, rxq = _dropin_ref(x, packed, N, K, 0.025, g)
+        same_bits(out, ref, "out K=%d N=%d" % (K, N))
+        same_bits(xn, rxn, "x_norm K=%d N=%d" % (K, N))
+        np.testing.assert_array_equal(xq[:K], rxq[:K])
+
+
+def test_dropin_single_token_registered(hip):
+    """The same entry on weights of a registered model image (1B and 255M
+    widths: in_proj 2048 -> 8384 and 1024 -> 4192, out_proj 4096 -> 2048 and
+    2048 -> 1024), several tokens in a row through each tensor."""
+    for dm, nh in ((2048, 64), (1024, 32)):
+        blob = bh.synth_model(1000, dm, 1, nh, 9, bh.SYNTH_UNIFORM)
+        _REGISTERED.append(blob)
+        assert hip.bm_hip_set_mmap(ptr(blob), blob.nbytes)
+        for which, norm in ((bh.BM_L_IN_PROJ, bh.BM_L_IN_NORM),
+                            (bh.BM_L_OUT_PROJ, bh.BM_L_OUT_NORM)):
+            w = bh.image_tensors(blob, 0, which)
+            nw = bh.image_tensors(blob, 0, norm)
+            K, N = w.cols, w.rows
+            packed = np.ctypeslib.as_array(C.cast(w.packed_data, C.POINTER(C.c_uint8)),
+                                           (N * (K // 4),)).reshape(N, K // 4)
+            g = np.ctypeslib.as_array(C.cast(nw.data, C.POINTER(C.c_float)), (K,))
+            for t in range(3):
+                note("drop-in registered dm=%d K=%d N=%d token %d" % (dm, K, N, t))
+                x = rnd(500 + t).standard_normal(K).astype(np.float32)
+                out, xn, xq = _dropin_call(hip, x, w, nw, N, K)
+                ref, rxn, rxq = _dropin_ref(x, packed, N, K, w.scale, g)
+                same_bits(out, ref, "out")
+                same_bits(xn, rxn, "x_norm")
+                np.testing.assert_array_equal(xq[:K], rxq[:K])
+
+
 def test_dropin_batch_golden_shapes(hip):
     z = np.load(os.path.join(GOLD, "bitlinear_shapes.npz"))
     for key in sorted(k[4:] for k in z.files if k.startswith("out_")):
@@ -349,4 +427,5 @@ def test_register_table(hip):
 
 def test_set_mmap_registers_model(hip):
     blob = bh.synth_model(1000, 128, 2, 4, 5, bh.SYNTH_RAW_BYTES)
+    _REGISTERED.append(blob)
     assert hip.bm_hip_set_mmap(ptr(blob), blob.nbytes)
