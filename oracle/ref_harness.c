@@ -258,3 +258,38 @@ int bmref_model_layer_state(void *h,
     memcpy(ssm_state, b->ssm_state, (size_t) b->d_inner * sizeof(float));
     return b->conv_pos;
 }
+
+/* ---------------------------------------------------------------------------
+ * The HIP backend wired into this build's own plugin table, as a reference
+ * tree built with HAS_HIP would do it (the table's types must agree): the
+ * caller passes bm_hip_register from libbitmamba_hip.so, which then owns
+ * rms_norm / bitlinear_forward / bitlinear_forward_batch and leaves
+ * bitlinear_prepare and bitlinear_row_worker NULL (src/dispatch.c:15-52,
+ * src/block.c:361-371, src/model.c:1258-1262).  bmref_init() restores the
+ * CPU table.
+ * ------------------------------------------------------------------------- */
+#define BM_HIP_HAVE_TENSOR_T
+#include "bm_hip.h"
+
+_Static_assert(sizeof(kernel_dispatch_t) == sizeof(bm_hip_dispatch_t),
+               "kernel_dispatch_t and bm_hip_dispatch_t must have one layout");
+
+int bmref_use_hip(bool (*reg)(bm_hip_dispatch_t *))
+{
+    return reg((bm_hip_dispatch_t *) &g_kernels) ? 1 : 0;
+}
+
+const char *bmref_kernels_name(void)
+{
+    return g_kernels.name;
+}
+
+/* the mmap'd model file of a loaded model (what bm_hip_set_mmap registers
+ * at the Metal spot of model_load, src/model.c:840-851) */
+int bmref_model_image(void *h, void **addr, size_t *size)
+{
+    const bitmamba_model_t *m = (const bitmamba_model_t *) h;
+    *addr = m->mmap_addr;
+    *size = m->mmap_size;
+    return m->mmap_addr != NULL;
+}

@@ -78,6 +78,9 @@ _REF_SIGS = {
     "bmref_model_logits": (C.POINTER(C.c_float), [_vp]),
     "bmref_model_vocab": (_i, [_vp]),
     "bmref_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
+    "bmref_use_hip": (_i, [_vp]),
+    "bmref_kernels_name": (C.c_char_p, []),
+    "bmref_model_image": (_i, [_vp, C.POINTER(_vp), C.POINTER(_sz)]),
 }
 
 _oracle = None
