@@ -13,6 +13,10 @@ Prints ONE JSON line.  Legs (all by default):
             prompt on the same model (prefill_1b: time to first token)
   sampled   the same model decoding with the device sampler (temp 0.8,
             min_p 0.05, top_p 0.9, top_k 40): tok/s of up to 128 steps
+  fast      opt-in fast mode (sums of squares as a pairwise tree): the same
+            greedy decode and 1024-token prefill, its first divergence from
+            the reference's stream, the 255M decode, and the quantizer
+            against parity at K = 1024, 2048, 4096 (4096 tokens each)
   roofline  the decode GEMV kernel (K=2048 in_proj shape) streaming 512 MiB
             of distinct weight rows in one launch, timed with HIP events on
             the library stream -> achieved GB/s vs 8 TB/s
@@ -91,7 +95,15 @@ class Events:
 SAMPLED = dict(temp=0.8, min_p=0.05, top_p=0.9, top_k=40, seed=42)
 
 
-def leg_decode(L, steps, warmup, sampled=False):
+def divergence(toks, ref):
+    """First step where two greedy streams differ (None if they agree over
+    their common length), and the reference record's top-2 margin there."""
+    n = min(len(toks), len(ref["tokens"]))
+    i = next((k for k in range(n) if int(toks[k]) != ref["tokens"][k]), None)
+    return i, (None if i is None else round(ref["top2_margin"][i], 5))
+
+
+def leg_decode(L, steps, warmup, sampled=False, fast=False):
     c = CFG_1B
     t0 = time.time()
     blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
@@ -135,17 +147,48 @@ def leg_decode(L, steps, warmup, sampled=False):
         L.bm_hip_synchronize()
         pf = min(pf, time.perf_counter() - t2)
     prefill = dict(tokens=1024, ms=round(pf * 1e3, 3), tok_s=round(1024 / pf, 1))
+    gold_path = os.path.join(ROOT, "tests", "golden", "stream_1b.json")
+    gold = json.load(open(gold_path)) if os.path.exists(gold_path) else None
+    fres = None
+    if fast:
+        # fast mode (pairwise-tree sums of squares) on the same model, greedy
+        m.reset()
+        m.set_sampler()
+        m.set_fast(1)
+        ffirst, _ = m.generate(prompt, warmup)
+        L.bm_hip_synchronize()
+        t3 = time.perf_counter()
+        fms = m.decode(steps)
+        L.bm_hip_synchronize()
+        fw = time.perf_counter() - t3
+        ftoks = np.concatenate([ffirst, m.tokens(steps)])
+        fpf = 1e9
+        for _ in range(3):
+            m.reset()
+            L.bm_hip_synchronize()
+            t2 = time.perf_counter()
+            m.prefill(long_prompt)
+            L.bm_hip_synchronize()
+            fpf = min(fpf, time.perf_counter() - t2)
+        m.set_fast(0)
+        fres = dict(tok_s=round(steps / fw, 2), ms_per_step=round(fw * 1e3 / steps, 4),
+                    device_ms_per_step=round(fms / steps, 4), steps=steps,
+                    tokens_identical_to_parity=ftoks.tolist() == toks.tolist(),
+                    prefill_1024_ms=round(fpf * 1e3, 3))
+        if gold:
+            i, mg = divergence(ftoks, gold)
+            fres.update(first_divergence_from_reference=i, reference_top2_margin_there=mg,
+                        compared_steps=min(len(ftoks), len(gold["tokens"])))
     m.free()
     match = None
-    gold = os.path.join(ROOT, "tests", "golden", "stream_1b.json")
-    if os.path.exists(gold):
-        ref = json.load(open(gold))["tokens"]
+    if gold:
+        ref = gold["tokens"]
         n = min(len(ref), len(toks))
         match = toks[:n].tolist() == ref[:n]
-    return wall, dev_ms, match, samp, prefill
+    return wall, dev_ms, match, samp, prefill, fres
 
 
-def leg_d255m(L):
+def leg_d255m(L, fast=False):
     c = CFG_255M
     blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
                           c["dist"])
@@ -155,16 +198,79 @@ def leg_d255m(L):
     m.generate(prompt, 4)                            # warm the step graph
     m.reset()
     toks, ms = m.generate(prompt, c["steps"])        # device time of the decode steps
+    fres = None
+    gold_path = os.path.join(ROOT, "tests", "golden", "stream_255m.json")
+    gold = json.load(open(gold_path)) if os.path.exists(gold_path) else None
+    if fast:
+        m.set_fast(1)
+        m.reset()
+        m.generate(prompt, 4)
+        m.reset()
+        ftoks, fms = m.generate(prompt, c["steps"])
+        fres = dict(tok_s=round(c["steps"] / (fms * 1e-3), 1),
+                    ms_per_step=round(fms / c["steps"], 4),
+                    tokens_identical_to_parity=ftoks.tolist() == toks.tolist())
+        if gold:
+            i, mg = divergence(ftoks, gold)
+            fres.update(first_divergence_from_reference=i, reference_top2_margin_there=mg)
     m.free()
     match = None
-    gold = os.path.join(ROOT, "tests", "golden", "stream_255m.json")
-    if os.path.exists(gold):
-        match = toks.tolist() == json.load(open(gold))["tokens"]
+    if gold:
+        match = toks.tolist() == gold["tokens"]
     bpt = packed_bytes_per_token(c)
     tok_s = c["steps"] / (ms * 1e-3)
-    return dict(tok_s=round(tok_s, 1), ms_per_step=round(ms / c["steps"], 4),
-                packed_weight_GBps=round(tok_s * bpt / 1e9, 1), packed_bytes_per_token=bpt,
-                tokens_match_reference=match, steps=c["steps"])
+    r = dict(tok_s=round(tok_s, 1), ms_per_step=round(ms / c["steps"], 4),
+             packed_weight_GBps=round(tok_s * bpt / 1e9, 1), packed_bytes_per_token=bpt,
+             tokens_match_reference=match, steps=c["steps"])
+    if fres:
+        r["fast_mode"] = fres
+    return r
+
+
+def leg_fast_quant(L, M=4096):
+    """Fast against parity quantization on the same rows (the parity kernel
+    is bit-exact with the reference's scalar quantizer): int8 mismatch rate,
+    scale_x drift, the fp32 BitLinear outputs' largest difference relative
+    to the output scale, and both quantizers' kernel time."""
+    out = {}
+    ev = Events(L)
+    r = np.random.default_rng(17)
+    for K, N in ((1024, 4192), (2048, 8384), (4096, 2048)):
+        x = r.standard_normal((M, K)).astype(np.float32)
+        g = (1.0 + 0.1 * r.standard_normal(K)).astype(np.float32)
+        w = bh.synth_ternary(K, 1, N, K, bh.SYNTH_P0_40)
+        dx, dg, dW = (bh.DeviceBuffer.from_array(a) for a in (x, g, w))
+        res = {}
+        for name, fn in (("parity", L.bm_hip_quantize_dev), ("fast", L.bm_hip_quantize_fast_dev)):
+            dq, ds = bh.DeviceBuffer(M * K), bh.DeviceBuffer(4 * M)
+            da = bh.DeviceBuffer(L.bm_hip_act_bytes(M, K))
+            do = bh.DeviceBuffer(4 * M * N)
+            q = lambda: bh.check(fn(dx.ptr, M, K, K, dg.ptr, None, dq.ptr, K, ds.ptr, da.ptr,
+                                    None), name)
+            q()
+            ev.start()
+            for _ in range(5):
+                q()
+            us = ev.stop_ms() * 1e3 / 5
+            bh.check(L.bm_hip_bitlinear_act_dev(da.ptr, ds.ptr, M, dW.ptr, N, K, 0.02, 0, do.ptr,
+                                                None), "product")
+            L.bm_hip_synchronize()
+            res[name] = (dq.download((M, K), np.int8), ds.download(M, np.float32),
+                         do.download((M, N), np.float32), us)
+            for b in (dq, ds, da, do):
+                b.free()
+        for b in (dx, dg, dW):
+            b.free()
+        (pq, ps, po, pus), (fq, fs, fo, fus) = res["parity"], res["fast"]
+        d = fq.astype(np.int32) - pq.astype(np.int32)
+        out["K%d" % K] = dict(
+            tokens=M, int8_mismatch_rate=float("%.3g" % (np.count_nonzero(d) / d.size)),
+            int8_max_abs_diff=int(np.abs(d).max()),
+            scale_x_max_rel_diff=float("%.3g" % np.max(np.abs(fs / ps - 1.0))),
+            out_max_abs_diff_over_max_abs=float("%.3g" % (np.max(np.abs(fo - po)) /
+                                                          np.max(np.abs(po)))),
+            quantize_us_parity=round(pus, 1), quantize_us_fast=round(fus, 1))
+    return out
 
 
 def gemv1_inputs():
@@ -665,7 +771,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--legs",
-                    default="decode,sampled,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
+                    default="decode,sampled,fast,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: the BitLinear hot path runs on exactly one GPU (there is no "
@@ -696,7 +802,11 @@ def main():
         sys.exit("bm_hip_init: " + bh.last_error())
     res = {}
     if "decode" in legs:
-        wall, dev_ms, match, samp, pf = leg_decode(L, a.steps, a.warmup, "sampled" in legs)
+        wall, dev_ms, match, samp, pf, fres = leg_decode(L, a.steps, a.warmup, "sampled" in legs,
+                                                         "fast" in legs)
+        res["fast"] = fres
+        if fres:
+            log("fast-mode decode: %s" % json.dumps(fres))
         res["decode"] = (wall, dev_ms, match)
         res["sampled"] = samp
         res["prefill_model"] = pf
@@ -717,7 +827,10 @@ def main():
             v["frac_of_ternary_ceiling"] = round(v["tops"] / mf["ternary_operands_tops"], 4)
     if pre:
         log("prefill: %s" % json.dumps(pre))
-    d255 = leg_d255m(L) if "d255m" in legs else None
+    d255 = leg_d255m(L, "fast" in legs) if "d255m" in legs else None
+    fq = leg_fast_quant(L) if "fast" in legs else None
+    if fq:
+        log("fast-mode quantizer: %s" % json.dumps(fq))
     if d255:
         log("255M-shape decode: %s" % json.dumps(d255))
     g1 = leg_gemv1(L) if "gemv1" in legs else None
@@ -763,6 +876,10 @@ def main():
         if strs:
             strs["cpu"] = cpu_of("stress")
     line["decode_sampled"] = res.get("sampled")
+    if res.get("fast") or fq:
+        line["decode_fast"] = dict(res.get("fast") or {}, quantizer=fq,
+                                   note="opt-in fast mode: sums of squares as a pairwise tree, "
+                                        "not the reference's bits; value stays parity mode")
     line["prefill_1b"] = res.get("prefill_model")
     line["roofline"] = roof
     line["mfma_ceiling"] = mf

@@ -78,6 +78,7 @@ SIGNATURES = {
     "bm_hip_mfma_peak_dev": (_i, [_i, _i, _i, _vp, _vp]),
     "bm_hip_act_bytes": (_sz, [_i, _i]),
     "bm_hip_quantize_dev": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
+    "bm_hip_quantize_fast_dev": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "bm_hip_bitlinear_act_dev": (_i, [_vp, _vp, _i, _vp, _i, _i, _f, _i, _vp, _vp]),
     "bm_hip_bitlinear_dev": (_i, [_vp, _i, _i, _vp, _vp, _i, _f, _i, _vp, _vp, _i, _vp, _vp,
                                   _vp]),
@@ -96,6 +97,7 @@ SIGNATURES = {
     "bm_hip_model_prefill": (_i, [_vp, _vp, _i]),
     "bm_hip_model_step": (_i, [_vp, _i, _vp, _i, _f]),
     "bm_hip_model_set_sampler": (_i, [_vp, _f, _f, _f, _i]),
+    "bm_hip_model_set_fast": (_i, [_vp, _i]),
     "bm_hip_model_seed": (_i, [_vp, _u64]),
     "bm_hip_sample_workspace_bytes": (_sz, [_i]),
     "bm_hip_sample_advanced": (_i, [_vp, _i, _f, _f, _f, _i, _vp, _vp, _vp, _vp]),
@@ -305,6 +307,9 @@ class Model:
         if n < 0:
             raise RuntimeError("generate: " + last_error())
         return out[:n].copy(), ms.value
+
+    def set_fast(self, on):
+        check(lib().bm_hip_model_set_fast(self.h, int(bool(on))), "set_fast")
 
     def prefill(self, tokens):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)

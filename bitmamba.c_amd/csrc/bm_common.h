@@ -47,11 +47,13 @@ extern "C" void bm_set_error(const char *fmt, ...);
 namespace bm {
 
 // nibbles = false leaves the split-nibble part of the workspace unwritten
-// (for products that read only the permuted bytes: product_reads_nibbles)
+// (for products that read only the permuted bytes: product_reads_nibbles);
+// fast = true sums the squares as a pairwise tree for n = 1024, 2048, 4096
+// (fast mode; other n keep the sequential sum)
 hipError_t launch_quantize(const float *x, int M, int n, int x_stride,
                            const float *gamma, float *x_norm, int8_t *xq,
                            int quant_stride, float *scale_x, uint8_t *act,
-                           hipStream_t s, bool nibbles = true);
+                           hipStream_t s, bool nibbles = true, bool fast = false);
 hipError_t launch_prep_i8(const int8_t *xq, int M, int ldx, int K, uint8_t *act,
                           hipStream_t s);
 // Output modes of the products: fp32 store, fp32 accumulate (out += o, the

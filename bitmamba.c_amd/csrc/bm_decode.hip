@@ -304,8 +304,20 @@ __device__ __forceinline__ void split_load(SplitIn<PRENORM>& in, const float* __
   }
 }
 
+// fast mode: 1/rms from the pairwise tree (one block barrier)
+template <int G>
+__device__ __forceinline__ float fast_rms(const float4 (&xv)[4], bool has, const Lds& l) {
+  constexpr int K = 1024 * G;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float w = wave_tree_f32(has ? sq_tree16(xv) : 0.0f);
+  if (lane == 0 && wave < G) l.bc[12 + wave] = w;
+  __syncthreads();
+  const float s = tree_top<G>(l.bc + 12);
+  return cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(s, 1.0f / K), 1e-6f)));
+}
+
 template <int G, bool PRENORM>
-__device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l,
+__device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l, bool fast,
                                 float* __restrict__ xn_out = nullptr,
                                 int8_t* __restrict__ xq_out = nullptr) {
   constexpr int NG = 1024 * G / 16;
@@ -315,14 +327,24 @@ __device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l,
   float4 (&xv)[4] = in.xv;
   const float4 (&gv)[4] = in.gv;
   const float4 (&gp)[PRENORM ? 4 : 1] = in.gp;
-  put_squares<G>(xv, has, l);
-  float rms = chain_rms<G>(l);
+  float rms;
+  if (fast) {
+    rms = fast_rms<G>(xv, has, l);
+  } else {
+    put_squares<G>(xv, has, l);
+    rms = chain_rms<G>(l);
+  }
   if constexpr (PRENORM) {
     // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
 #pragma unroll
     for (int k = 0; k < 4; ++k) xv[k] = scale4(xv[k], rms, gp[k]);
-    put_squares<G>(xv, has, l);
-    rms = chain_rms<G>(l);
+    if (fast) {
+      __syncthreads();  // the first tree's sums are read before they are replaced
+      rms = fast_rms<G>(xv, has, l);
+    } else {
+      put_squares<G>(xv, has, l);
+      rms = chain_rms<G>(l);
+    }
   }
   // int8 quantization (src/kernel.c:93-128, 358-386)
   float mx = 0.0f;
@@ -451,7 +473,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
                                                     float w_scale, float* __restrict__ out,
                                                     float* __restrict__ part_v,
                                                     int* __restrict__ part_i, float temp,
-                                                    DropOut dr) {
+                                                    int fast, DropOut dr) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int RPW = 64 / T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -502,7 +524,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   int8_t* const xq_out = DROP && b == 0 ? dr.xq : nullptr;
   float scale_x;
   if constexpr (WP) {
-    scale_x = split_prologue<C, PRENORM>(sin, l, xn_out, xq_out);
+    scale_x = split_prologue<C, PRENORM>(sin, l, fast != 0, xn_out, xq_out);
   } else {
     float rms = pro_rms<C>(sx, K, l);
     if constexpr (PRENORM) {
@@ -648,7 +670,7 @@ template <int T, int P, int NPF, int C, bool WP>
 __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma,
                                                     const uint8_t* __restrict__ W, float w_scale,
-                                                    SsmArgs a) {
+                                                    SsmArgs a, int fast) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float s_proj[kRowsCB];
   constexpr int RPW = 64 / T;
@@ -705,7 +727,7 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   const Lds l = lds_carve(lds, K);
   float scale_x;
   if constexpr (WP) {
-    scale_x = split_prologue<C, false>(sin, l);
+    scale_x = split_prologue<C, false>(sin, l, fast != 0);
   } else {
     const float rms = pro_rms<C>(sx, K, l);
     scale_x = pro_quant<C>(sx, sg, rms, K, l);
@@ -879,31 +901,32 @@ static int rows_blocks(int N, int K) {
 template <int NPF, bool PRENORM, int MODE, int PICK, bool DROP = false>
 static hipError_t rows_t(const float* x, int K, const float* gpre, const float* g,
                          const uint8_t* W, int N, float w_scale, float* out, float* pv, int* pi,
-                         hipStream_t s, float temp = 1.0f, DropOut dr = DropOut{}) {
+                         hipStream_t s, float temp = 1.0f, DropOut dr = DropOut{},
+                         bool fast = false) {
   const size_t lds = lds_bytes(K);
   const dim3 grid(rows_blocks<NPF>(N, K)), block(256);
   if (K % 64 != 0) return hipErrorInvalidValue;
   if (K == 1024)
     hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else if (K == 2048)
     hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else if (K == 4096)
     hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
-                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else if (K <= 1024)
     hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, false, DROP>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else if (K <= 2048)
     hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, false, DROP>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else if (K <= 4096)
     hipLaunchKernelGGL((k_rows_fused<64, 1, NPF, 4, PRENORM, MODE, PICK, false, DROP>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else if (K <= 8192)
     hipLaunchKernelGGL((k_rows_fused<64, 2, NPF, 8, PRENORM, MODE, PICK, false, DROP>), grid, block,
-                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, dr);
+                       lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -911,15 +934,16 @@ static hipError_t rows_t(const float* x, int K, const float* gpre, const float* 
 
 // proj = BitLinear(x) over the per-head in_proj rows
 hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_t* W, int N,
-                         float w_scale, float* proj, hipStream_t s) {
+                         float w_scale, float* proj, hipStream_t s, bool fast) {
   return rows_t<4, false, 0, 0>(x, K, nullptr, gamma, W, N, w_scale, proj, nullptr, nullptr,
-                                    s);
+                                    s, 1.0f, DropOut{}, fast);
 }
 
 // x += BitLinear(y)  (out_proj with the residual add)
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
-                          float w_scale, float* x, hipStream_t s) {
-  return rows_t<2, false, 1, 0>(y, K, nullptr, gamma, W, N, w_scale, x, nullptr, nullptr, s);
+                          float w_scale, float* x, hipStream_t s, bool fast) {
+  return rows_t<2, false, 1, 0>(y, K, nullptr, gamma, W, N, w_scale, x, nullptr, nullptr, s,
+                                1.0f, DropOut{}, fast);
 }
 
 bool inproj_ssm_fits(int K, int hd) { return K % 64 == 0 && K <= 8192 && hd % kCB == 0; }
@@ -941,32 +965,33 @@ hipError_t launch_dropin(const float* x, int K, const float* gamma, const uint8_
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
                              const float* cw, const float* cb, float* cs, float* ssm,
-                             const float* D, float* y, const int* ctl, hipStream_t s) {
+                             const float* D, float* y, const int* ctl, hipStream_t s,
+                             bool fast) {
   if (!inproj_ssm_fits(K, hd)) return hipErrorInvalidValue;
   const SsmArgs args{dt_bias, A, cw, cb, cs, ssm, D, y, ctl, hd, nh * hd};
   const dim3 grid(nh * (hd / kCB)), block(256);
   const size_t lds = lds_bytes(K);
   if (K == 1024)
     hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, true>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   else if (K == 2048)
     hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, true>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   else if (K == 4096)
     hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, true>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   else if (K <= 1024)
     hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   else if (K <= 2048)
     hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   else if (K <= 4096)
     hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   else
     hipLaunchKernelGGL((k_inproj_ssm<64, 2, 9, 8, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args);
+                       w_scale, args, (int)fast);
   return hipGetLastError();
 }
 
@@ -989,15 +1014,15 @@ int lm_head_blocks(int N, int K) { return rows_blocks<kLmNpf>(N, K); }
 // part_i), 2 logits times 1/temp with the blocks' maxima (part_v)
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
                           const uint8_t* W, int N, float w_scale, float* logits, int pick,
-                          float temp, float* part_v, int* part_i, hipStream_t s) {
+                          float temp, float* part_v, int* part_i, hipStream_t s, bool fast) {
   if (pick == 1)
     return rows_t<kLmNpf, true, 0, 1>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
-                                  s);
+                                      s, 1.0f, DropOut{}, fast);
   if (pick == 2)
     return rows_t<kLmNpf, true, 0, 2>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, nullptr,
-                                  s, temp);
+                                      s, temp, DropOut{}, fast);
   return rows_t<kLmNpf, true, 0, 0>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr, nullptr,
-                                s);
+                                    s, 1.0f, DropOut{}, fast);
 }
 
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,

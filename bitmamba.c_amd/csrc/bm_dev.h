@@ -136,6 +136,44 @@ __device__ __forceinline__ int row_total_i32(int part, int xs_slice, int unit_ba
 // wave 0 own chain j in segments of E consecutive elements; each lane adds
 // its segment to the running sum, which then moves one lane up the 16-lane
 // row (DPP row_shr:1).  After 16 rounds lane 16j+15 holds chain j's sum.
+// ---------------------------------------------------------------------------
+// Fast mode (opt-in, not the reference's bits): the sum of squares as one
+// balanced pairwise tree over the columns -- 16 consecutive columns per
+// leaf group, (((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)))+..., then the groups
+// pairwise in index order -- in place of the four sequential chains.  The
+// same tree in every kernel that offers the mode, so a token's prefill and
+// decode normalize alike.  (The reduction class of the Metal backend's
+// rms_norm_quantize, src/metal/bm_shaders.metal:40-60, not its order.)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sq_tree16(const float4 (&v)[4]) {
+  float t[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    t[k] = __fadd_rn(__fadd_rn(__fmul_rn(v[k].x, v[k].x), __fmul_rn(v[k].y, v[k].y)),
+                     __fadd_rn(__fmul_rn(v[k].z, v[k].z), __fmul_rn(v[k].w, v[k].w)));
+  return __fadd_rn(__fadd_rn(t[0], t[1]), __fadd_rn(t[2], t[3]));
+}
+
+// pairwise over the 16 lanes of each row (every butterfly step adds two
+// equal-sized halves, so all lanes of the row hold the same bits), then the
+// four rows pairwise: the tree over the wave's 64 leaf groups
+__device__ __forceinline__ float wave_tree_f32(float v) {
+  v = __fadd_rn(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+  v = __fadd_rn(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+  v = __fadd_rn(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+  v = __fadd_rn(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
+  return __fadd_rn(__fadd_rn(lane_f32(v, 0), lane_f32(v, 16)),
+                   __fadd_rn(lane_f32(v, 32), lane_f32(v, 48)));
+}
+
+// the tree's top levels over the G wave sums (1024 columns each)
+template <int G>
+__device__ __forceinline__ float tree_top(const float* w) {
+  if constexpr (G == 1) return w[0];
+  if constexpr (G == 2) return __fadd_rn(w[0], w[1]);
+  return __fadd_rn(__fadd_rn(w[0], w[1]), __fadd_rn(w[2], w[3]));
+}
+
 __host__ __device__ inline bool chain_in_regs(int K) { return K == 1024 || K == 2048 || K == 4096; }
 __host__ __device__ inline int sq_stride_of(int K) { return K / 4 + 68; }
 

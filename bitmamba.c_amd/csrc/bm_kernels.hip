@@ -155,7 +155,8 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
                                                        int8_t* __restrict__ xq, int quant_stride,
                                                        float* __restrict__ scale_out,
                                                        uint8_t* __restrict__ act,
-                                                       size_t act_stride, bool nib) {
+                                                       size_t act_stride, bool nib,
+                                                       bool fast) {
   constexpr int K = 1024 * G, E = K / 64;
   extern __shared__ __attribute__((aligned(16))) float lds_sq[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -174,33 +175,42 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
       xv[i][k] = ((const float4*)xr)[c4];
       gv[i][k] = ((const float4*)gamma)[c4];
     }
-  // column 16g + 4k + j is element 4g + k of chain j (segments of E padded
-  // by 4 floats)
+  float sum;
+  if (fast) {
+    // the pairwise tree: leaf group lane + 64 i, then the G wave sums
+    float w[G];
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const int e = 4 * (lane + 64 * i);
-    const int pe = e + 4 * (e / E);
-    const float4* v = xv[i];
-    *(float4*)&sq[pe] = make_float4(__fmul_rn(v[0].x, v[0].x), __fmul_rn(v[1].x, v[1].x),
-                                    __fmul_rn(v[2].x, v[2].x), __fmul_rn(v[3].x, v[3].x));
-    *(float4*)&sq[stride + pe] = make_float4(__fmul_rn(v[0].y, v[0].y), __fmul_rn(v[1].y, v[1].y),
-                                             __fmul_rn(v[2].y, v[2].y), __fmul_rn(v[3].y, v[3].y));
-    *(float4*)&sq[2 * stride + pe] =
-        make_float4(__fmul_rn(v[0].z, v[0].z), __fmul_rn(v[1].z, v[1].z),
-                    __fmul_rn(v[2].z, v[2].z), __fmul_rn(v[3].z, v[3].z));
-    *(float4*)&sq[3 * stride + pe] =
-        make_float4(__fmul_rn(v[0].w, v[0].w), __fmul_rn(v[1].w, v[1].w),
-                    __fmul_rn(v[2].w, v[2].w), __fmul_rn(v[3].w, v[3].w));
+    for (int i = 0; i < G; ++i) w[i] = wave_tree_f32(sq_tree16(xv[i]));
+    sum = tree_top<G>(w);
+  } else {
+    // column 16g + 4k + j is element 4g + k of chain j (segments of E padded
+    // by 4 floats)
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int e = 4 * (lane + 64 * i);
+      const int pe = e + 4 * (e / E);
+      const float4* v = xv[i];
+      *(float4*)&sq[pe] = make_float4(__fmul_rn(v[0].x, v[0].x), __fmul_rn(v[1].x, v[1].x),
+                                      __fmul_rn(v[2].x, v[2].x), __fmul_rn(v[3].x, v[3].x));
+      *(float4*)&sq[stride + pe] = make_float4(__fmul_rn(v[0].y, v[0].y), __fmul_rn(v[1].y, v[1].y),
+                                               __fmul_rn(v[2].y, v[2].y), __fmul_rn(v[3].y, v[3].y));
+      *(float4*)&sq[2 * stride + pe] =
+          make_float4(__fmul_rn(v[0].z, v[0].z), __fmul_rn(v[1].z, v[1].z),
+                      __fmul_rn(v[2].z, v[2].z), __fmul_rn(v[3].z, v[3].z));
+      *(float4*)&sq[3 * stride + pe] =
+          make_float4(__fmul_rn(v[0].w, v[0].w), __fmul_rn(v[1].w, v[1].w),
+                      __fmul_rn(v[2].w, v[2].w), __fmul_rn(v[3].w, v[3].w));
+    }
+    // one wave's LDS operations complete in order; the fences keep the
+    // compiler from moving the reads above the writes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float cs = chain_regs<E>(sq, stride, lane);
+    const float s0 = lane_f32(cs, 15), s1 = lane_f32(cs, 31);
+    const float s2 = lane_f32(cs, 47), s3 = lane_f32(cs, 63);
+    sum = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
   }
-  // one wave's LDS operations complete in order; the fences keep the
-  // compiler from moving the reads above the writes
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const float cs = chain_regs<E>(sq, stride, lane);
-  const float s0 = lane_f32(cs, 15), s1 = lane_f32(cs, 31);
-  const float s2 = lane_f32(cs, 47), s3 = lane_f32(cs, 63);
-  const float sum = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
   // sum / K with K a power of two: an exact scaling, rounded like the division
   const float rms = cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(sum, 1.0f / K), 1e-6f)));
 
@@ -1004,7 +1014,7 @@ __global__ void k_canonicalize_tail(uint8_t* __restrict__ p, size_t n) {
 // ---------------------------------------------------------------------------
 hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const float* gamma,
                            float* x_norm, int8_t* xq, int quant_stride, float* scale_x,
-                           uint8_t* act, hipStream_t s, bool nibbles) {
+                           uint8_t* act, hipStream_t s, bool nibbles, bool fast) {
   if (M <= 0) return hipSuccess;
   // one wave per token when the rows allow 16-byte loads of whole groups
   const bool aligned = ((uintptr_t)x % 16 == 0) && (x_stride % 4 == 0) &&
@@ -1015,13 +1025,13 @@ hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const flo
     const size_t lds = quantize_wave_lds(n);
     if (n == 1024)
       hipLaunchKernelGGL(k_quantize_wave<1>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
-                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles);
+                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles, fast);
     else if (n == 2048)
       hipLaunchKernelGGL(k_quantize_wave<2>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
-                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles);
+                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles, fast);
     else
       hipLaunchKernelGGL(k_quantize_wave<4>, grid, block, lds, s, x, M, x_stride, gamma, x_norm,
-                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles);
+                         xq, quant_stride, scale_x, act, act_row_bytes(n), nibbles, fast);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_quantize, dim3(M), dim3(QT), 0, s, x, n, x_stride, gamma, x_norm, xq,

@@ -343,21 +343,22 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ 
 }
 
 hipError_t launch_inproj(const float* x, int K, const float* gamma, const uint8_t* W, int N,
-                         float w_scale, float* proj, hipStream_t s);
+                         float w_scale, float* proj, hipStream_t s, bool fast);
 hipError_t launch_outproj(const float* y, int K, const float* gamma, const uint8_t* W, int N,
-                          float w_scale, float* x, hipStream_t s);
+                          float w_scale, float* x, hipStream_t s, bool fast);
 bool inproj_ssm_fits(int K, int hd);
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
                              const float* cw, const float* cb, float* cs, float* ssm,
-                             const float* D, float* y, const int* ctl, hipStream_t s);
+                             const float* D, float* y, const int* ctl, hipStream_t s,
+                             bool fast);
 hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
                             const float* A, const float* cw, const float* cb, float* cs,
                             float* ssm, const float* D, float* y, const int* ctl, hipStream_t s);
 int lm_head_blocks(int N, int K);
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
                           const uint8_t* W, int N, float w_scale, float* logits, int pick,
-                          float temp, float* part_v, int* part_i, hipStream_t s);
+                          float temp, float* part_v, int* part_i, hipStream_t s, bool fast);
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,
                        int* out_tokens, const float* embed, int dm, float* x, hipStream_t s);
 size_t sample_scratch_bytes(int V);
@@ -425,6 +426,8 @@ struct bm_hip_model {
   // BM_HIP_NO_GRAPH=1: enqueue each step's kernels directly instead of
   // replaying the captured graph (for tools that cannot trace graphs)
   bool no_graph = false;
+  // fast mode (bm_hip_model_set_fast): sums of squares as a pairwise tree
+  bool fast = false, graph_fast = false;
 };
 
 namespace {
@@ -447,12 +450,12 @@ int bitlinear(bm_hip_model* m, const float* x, int M, int K, const float* norm,
               float* sc, int8_t* xq, hipStream_t s) {
   const bool generic = bm::product_needs_generic(M, K);
   MCHECK(bm::launch_quantize(x, M, K, K, norm, nullptr, generic ? xq : nullptr, K, sc,
-                             generic ? nullptr : act, s, bm::product_reads_nibbles(M, N, K)));
+                             generic ? nullptr : act, s, bm::product_reads_nibbles(M, N, K),
+                             m->fast));
   if (generic)
     MCHECK(bm::launch_generic(xq, K, sc, M, W, N, K, scale, out, mode, s));
   else
     MCHECK(bm::launch_product(act, sc, M, W, N, K, scale, true, out, mode, s));
-  (void)m;
   return 0;
 }
 
@@ -472,11 +475,11 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
     if (bm::inproj_ssm_fits(dm, m->hd)) {
       MCHECK(bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
                                    Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
-                                   m->ctl, s));
+                                   m->ctl, s, m->fast));
     } else {
       if (rows_dm) {
         MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
-                                 s));
+                                 s, m->fast));
       } else if (bitlinear(m, m->x, 1, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
                            bm::MODE_STORE, m->act, m->scale, m->xq, s)) {
         return -1;
@@ -485,7 +488,8 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
                                   Ly.conv_b, cs, ss, Ly.D, m->y, m->ctl, s));
     }
     if (rows_di) {
-      MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s));
+      MCHECK(bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s,
+                                m->fast));
     } else if (bitlinear(m, m->y, 1, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x,
                          bm::MODE_ACC, m->act, m->scale, m->xq, s)) {
       return -1;
@@ -499,7 +503,7 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
   if (rows_dm) {
     MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab,
                               m->lm_scale, m->logits, fused_pick ? 1 : (fused_scale ? 2 : 0),
-                              m->temp, m->part_v, m->part_i, s));
+                              m->temp, m->part_v, m->part_i, s, m->fast));
   } else {
     // rms_norm(norm_f), then BitLinear with lm_head.norm (src/model.c:1225, 1259-1261)
     MCHECK(bm::launch_rms_norm(m->x, dm, m->norm_f, m->feat, m->scale + 8, s));
@@ -543,7 +547,7 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
   }
   const float samp[4] = {m->temp, m->min_p, m->top_p, (float)m->top_k};
   if (m->exec && m->graph_penalty == penalty && m->graph_with_out == write_out &&
-      memcmp(samp, m->graph_samp, sizeof(samp)) == 0)
+      m->graph_fast == m->fast && memcmp(samp, m->graph_samp, sizeof(samp)) == 0)
     return 0;
   if (m->exec) {
     (void)hipGraphExecDestroy(m->exec);
@@ -566,6 +570,7 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
   MCHECK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
   m->graph_penalty = penalty;
   m->graph_with_out = write_out;
+  m->graph_fast = m->fast;
   memcpy(m->graph_samp, samp, sizeof(samp));
   return 0;
 }
@@ -915,6 +920,11 @@ extern "C" int bm_hip_model_set_sampler(bm_hip_model_t* m, float temp, float min
   m->min_p = min_p;
   m->top_p = top_p;
   m->top_k = top_k;
+  return 0;
+}
+
+extern "C" int bm_hip_model_set_fast(bm_hip_model_t* m, int on) {
+  m->fast = on != 0;
   return 0;
 }
 

@@ -557,9 +557,9 @@ extern "C" size_t bm_hip_act_bytes(int M, int n) {
 
 extern "C" size_t bm_hip_i8_act_bytes(int M, int K) { return bm_hip_act_bytes(M, K); }
 
-extern "C" int bm_hip_quantize_dev(const float* x, int M, int n, int x_stride,
-                                   const float* norm_w, float* x_norm, int8_t* x_quant,
-                                   int quant_stride, float* scale_x, void* act, void* stream) {
+static int quantize_dev(const float* x, int M, int n, int x_stride, const float* norm_w,
+                        float* x_norm, int8_t* x_quant, int quant_stride, float* scale_x,
+                        void* act, void* stream, bool fast) {
   if (!bm_hip_init()) return -1;
   if (M < 0 || n <= 0 || x_stride < n || !x || !norm_w || !scale_x ||
       (x_quant && quant_stride < n)) {
@@ -571,9 +571,25 @@ extern "C" int bm_hip_quantize_dev(const float* x, int M, int n, int x_stride,
     return -2;
   }
   BM_HIP_CHECK_RET(bm::launch_quantize(x, M, n, x_stride, norm_w, x_norm, x_quant, quant_stride,
-                                       scale_x, (uint8_t*)act, stream_or_default(stream)),
+                                       scale_x, (uint8_t*)act, stream_or_default(stream), true,
+                                       fast),
                    -1);
   return 0;
+}
+
+extern "C" int bm_hip_quantize_dev(const float* x, int M, int n, int x_stride,
+                                   const float* norm_w, float* x_norm, int8_t* x_quant,
+                                   int quant_stride, float* scale_x, void* act, void* stream) {
+  return quantize_dev(x, M, n, x_stride, norm_w, x_norm, x_quant, quant_stride, scale_x, act,
+                      stream, false);
+}
+
+extern "C" int bm_hip_quantize_fast_dev(const float* x, int M, int n, int x_stride,
+                                        const float* norm_w, float* x_norm, int8_t* x_quant,
+                                        int quant_stride, float* scale_x, void* act,
+                                        void* stream) {
+  return quantize_dev(x, M, n, x_stride, norm_w, x_norm, x_quant, quant_stride, scale_x, act,
+                      stream, true);
 }
 
 extern "C" int bm_hip_bitlinear_act_dev(const void* act, const float* scale_x, int M,

@@ -186,6 +186,24 @@ int bm_hip_quantize_dev(const float *x,
                         void *act,
                         void *stream);
 
+/* Fast mode of the same (opt-in; not the reference's bits): the sum of
+ * squares as one pairwise tree over the n values -- the reduction class of
+ * the Metal backend's rms_norm_quantize (src/metal/bm_shaders.metal:40-60)
+ * -- instead of the scalar kernel's four sequential chains
+ * (src/kernel.c:77-89).  For n = 1024, 2048, 4096; other n give the
+ * sequential sum. */
+int bm_hip_quantize_fast_dev(const float *x,
+                             int M,
+                             int n,
+                             int x_stride,
+                             const float *norm_w,
+                             float *x_norm,
+                             int8_t *x_quant,
+                             int quant_stride,
+                             float *scale_x,
+                             void *act,
+                             void *stream);
+
 /* Ternary BitLinear product on quantized activations (the act workspace
  * from bm_hip_quantize_dev): out[m*N + r] (fp32) with the scalar kernel's
  * 1024-column block epilogue (src/kernel.c:255-256, 407-447), bit-exact.
@@ -324,6 +342,13 @@ int bm_hip_model_step(bm_hip_model_t *m,
                       const int *history,
                       int history_len,
                       float penalty);
+/* Fast mode (on != 0; off by default): every later prefill, step,
+ * generate and decode sums the squares of each RMSNorm of d_model 1024,
+ * 2048 or 4096 (and d_inner of the same) as a pairwise tree, as
+ * bm_hip_quantize_fast_dev does, instead of the reference's sequential
+ * chains.  Results then differ from the reference in the last bits of
+ * 1/rms and occasionally by one int8 step.  0. */
+int bm_hip_model_set_fast(bm_hip_model_t *m, int on);
 /* Sampling parameters of every later step, generate and decode: the
  * temp, min_p, top_p, top_k arguments of model_forward_step
  * (src/model.c:1175-1183), sampled on the device by sample_advanced
