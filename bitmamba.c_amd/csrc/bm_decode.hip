@@ -262,12 +262,19 @@ __device__ __forceinline__ void put_squares(const float4 (&v)[4], bool has, cons
 }
 
 // rms = 1/sqrtf(sum/K + 1e-6f) from the squares in LDS; wave 0 runs the
-// chains, the result is broadcast through LDS (src/kernel.c:77-91)
-template <int G>
-__device__ __forceinline__ float chain_rms(const Lds& l) {
+// chains, the result is broadcast through LDS (src/kernel.c:77-91); the
+// other waves run `idle` meanwhile
+struct NoWork {
+  __device__ void operator()() const {}
+};
+
+template <int G, typename F = NoWork>
+__device__ __forceinline__ float chain_rms(const Lds& l, F&& idle = NoWork{}) {
   constexpr int K = 1024 * G, E = K / 64;
   __syncthreads();
-  if (threadIdx.x < 64) {
+  if (threadIdx.x >= 64) {
+    idle();
+  } else {
     const float cs = chain_regs<E>(l.sq, l.stride, threadIdx.x);
     const float s0 = lane_f32(cs, 15), s1 = lane_f32(cs, 31);
     const float s2 = lane_f32(cs, 47), s3 = lane_f32(cs, 63);
@@ -316,10 +323,12 @@ __device__ __forceinline__ float fast_rms(const float4 (&xv)[4], bool has, const
   return cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(s, 1.0f / K), 1e-6f)));
 }
 
-template <int G, bool PRENORM>
+// idle: work for waves 1.. while wave 0 runs the first chain (the first
+// fast-mode tree has no such window: they run it at once)
+template <int G, bool PRENORM, typename F = NoWork>
 __device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l, bool fast,
                                 float* __restrict__ xn_out = nullptr,
-                                int8_t* __restrict__ xq_out = nullptr) {
+                                int8_t* __restrict__ xq_out = nullptr, F&& idle = NoWork{}) {
   constexpr int NG = 1024 * G / 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool has = tid < NG;
@@ -329,10 +338,11 @@ __device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l, bool fast,
   const float4 (&gp)[PRENORM ? 4 : 1] = in.gp;
   float rms;
   if (fast) {
+    if (threadIdx.x >= 64) idle();
     rms = fast_rms<G>(xv, has, l);
   } else {
     put_squares<G>(xv, has, l);
-    rms = chain_rms<G>(l);
+    rms = chain_rms<G>(l, idle);
   }
   if constexpr (PRENORM) {
     // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
@@ -497,18 +507,27 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   }
 
   uint4 wv[NPF][P];
+  auto load_rows = [&]() {
 #pragma unroll
-  for (int it = 0; it < NPF; ++it) {
-    const int grp = g0 + wave + 4 * it;
-    const int r = grp * RPW + sub;
+    for (int it = 0; it < NPF; ++it) {
+      const int grp = g0 + wave + 4 * it;
+      const int r = grp * RPW + sub;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int j = p * T + u;
-      wv[it][p] = (grp < g1 && r < N && j < chunks)
-                      ? *(const uint4*)(W + (size_t)r * wstride + 16 * j)
-                      : make_uint4(0, 0, 0, 0);
+      for (int p = 0; p < P; ++p) {
+        const int j = p * T + u;
+        wv[it][p] = (grp < g1 && r < N && j < chunks)
+                        ? *(const uint4*)(W + (size_t)r * wstride + 16 * j)
+                        : make_uint4(0, 0, 0, 0);
+      }
     }
-  }
+  };
+  // The LM head streams more weight bytes than the memory pipeline takes
+  // at once, so issuing a wave's loads stalls that wave until most of them
+  // have arrived: there the waves issue their rows once the input's squares
+  // are in LDS (waves 1.. while wave 0 runs the first chain, wave 0 after
+  // the prologue), so the chains start at once.
+  constexpr bool defer_rows = PRENORM && WP;
+  if (!defer_rows) load_rows();
 
   // MODE 1: the residual values of the prefetched rows, read now so that
   // the final x += o does not wait for them
@@ -524,7 +543,10 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   int8_t* const xq_out = DROP && b == 0 ? dr.xq : nullptr;
   float scale_x;
   if constexpr (WP) {
-    scale_x = split_prologue<C, PRENORM>(sin, l, fast != 0, xn_out, xq_out);
+    if constexpr (defer_rows)
+      scale_x = split_prologue<C, PRENORM>(sin, l, fast != 0, xn_out, xq_out, load_rows);
+    else
+      scale_x = split_prologue<C, PRENORM>(sin, l, fast != 0, xn_out, xq_out);
   } else {
     float rms = pro_rms<C>(sx, K, l);
     if constexpr (PRENORM) {
@@ -537,6 +559,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       scale_x = pro_quant<C>(sx, sg, rms, K, l, xn_out, xq_out);
     }
   }
+  if (defer_rows && wave == 0) load_rows();
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
   int xsl[P];
@@ -882,7 +905,24 @@ __global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
   }
   __syncthreads();
   const int tok = s_tok;
-  for (int i = tid; i < dm; i += blockDim.x) x[i] = embed[(size_t)tok * dm + i];
+  const float* __restrict__ row = embed + (size_t)tok * dm;
+  if (dm % 4 == 0 && dm <= 4 * 4 * 256) {
+    // every load of the row in flight before the first store (16-byte
+    // rows: the embedding table and x are 256-byte aligned, dm % 4 == 0)
+    float4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = tid + 256 * k;
+      v[k] = 4 * i < dm ? ((const float4*)row)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = tid + 256 * k;
+      if (4 * i < dm) ((float4*)x)[i] = v[k];
+    }
+  } else {
+    for (int i = tid; i < dm; i += blockDim.x) x[i] = row[i];
+  }
 }
 
 // ---------------------------------------------------------------------------
