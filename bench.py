@@ -419,8 +419,42 @@ def leg_stress(L, reps=10):
         for b in (dx, da, do):
             b.free()
     dW.free()
-    out["note"] = ("int8 prep + product per call, canonical=0 (code 11 handled in-kernel); the "
-                   "16.8 MB weight tensor stays cache-resident across calls")
+    # cold: 32 distinct copies of the tensor (537 MB, more than the 256 MB
+    # last-level cache), one per call in turn, so every call streams its
+    # weights from HBM
+    n_copies = 32
+    cold = [bh.DeviceBuffer(N * K // 4) for _ in range(n_copies)]
+    w = bh.synth_ternary(5, 1, N, K, bh.SYNTH_P0_60)
+    src = bh.DeviceBuffer.from_array(w)
+    del w
+    for c in cold:
+        bh.check(L.bm_hip_copy_dev(c.ptr, src.ptr, N * K // 4, None), "copy")
+    src.free()
+    for M in (1, 16):
+        xq = bh.synth_int8(5, 2, (M, K))
+        dx = bh.DeviceBuffer.from_array(xq)
+        da = bh.DeviceBuffer(L.bm_hip_i8_act_bytes(M, K))
+        do = bh.DeviceBuffer(4 * M * N)
+        call = lambda c: bh.check(L.bm_hip_ternary_gemm_i32_dev(dx.ptr, M, K, c.ptr, N, K, 0,
+                                                                do.ptr, da.ptr, None), "stress")
+        for c in cold:
+            call(c)
+        ev.start()
+        for rep in range(2):
+            for c in cold:
+                call(c)
+        us = ev.stop_ms() * 1e3 / (2 * n_copies)
+        out["M%d" % M]["cold_us"] = round(us, 2)
+        out["M%d" % M]["weight_GBps_cold"] = round(N * K / 4 / (us * 1e-6) / 1e9, 1)
+        out["M%d" % M]["weight_frac_of_hbm_cold"] = round(N * K / 4 / (us * 1e-6) / 1e9 /
+                                                          HBM_PEAK_GBPS, 4)
+        for b in (dx, da, do):
+            b.free()
+    for c in cold:
+        c.free()
+    out["note"] = ("int8 prep + product per call, canonical=0 (code 11 handled in-kernel); warm: "
+                   "the one 16.8 MB weight tensor stays cache-resident across calls; cold: 32 "
+                   "copies (537 MB) used in turn, so each call streams its weights from HBM")
     return out
 
 
@@ -459,6 +493,48 @@ def leg_roofline(L, reps=5):
                 kernel="k_gemv<T=32,P=1,GW=8,canonical,store> (K=2048 decode GEMV, 8 row groups per wave)",
                 bytes_per_launch=wbytes, launch_us=round(ms * 1e3, 2),
                 rows_per_launch=N)
+
+
+DECODE_PROFILE = os.path.join(ROOT, "profiles", "decode_1b_kernels.txt")
+
+
+def decode_kernel_avg_us(name):
+    """Average duration of a decode kernel from the committed rocprofv3
+    summary of the same decode (its kernel-stats table)."""
+    try:
+        lines = open(DECODE_PROFILE).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        f = line.split()
+        if name in line and len(f) > 5:
+            try:
+                int(f[-5])
+                return float(f[-4])
+            except ValueError:
+                continue
+    return None
+
+
+def roofline_decode(c, dev_ms_per_step):
+    """The headline decode against HBM: the packed weight bytes of one token
+    over the device time of a step, and its dominant kernel (the in_proj +
+    SSM kernel: a layer's in_proj rows per launch) from the profile."""
+    dm, di, nh = c["d_model"], 2 * c["d_model"], c["n_heads"]
+    bpt = packed_bytes_per_token(c)
+    ach = bpt / (dev_ms_per_step * 1e-3) / 1e9
+    r = dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+             frac=round(ach / HBM_PEAK_GBPS, 4), bytes_per_token=bpt,
+             device_ms_per_step=dev_ms_per_step)
+    avg = decode_kernel_avg_us("k_inproj_ssm")
+    if avg:
+        inproj_bytes = (2 * di + 3 * nh) * dm // 4
+        k_ach = inproj_bytes / (avg * 1e-6) / 1e9
+        r["dominant_kernel"] = dict(name="k_inproj_ssm (in_proj quantize + GEMV + SSM step)",
+                                    bytes_per_launch=inproj_bytes, avg_us=avg,
+                                    achieved=round(k_ach, 1), frac=round(k_ach / HBM_PEAK_GBPS, 4),
+                                    source="profiles/decode_1b_kernels.txt")
+    return r
 
 
 def measured_traffic(rows):
@@ -875,6 +951,8 @@ def main():
                 pre[k]["cpu"] = cpu_of("gemm_" + k)
         if strs:
             strs["cpu"] = cpu_of("stress")
+    if "decode" in res:
+        line["roofline_decode"] = roofline_decode(CFG_1B, line["device_ms_per_step"])
     line["decode_sampled"] = res.get("sampled")
     if res.get("fast") or fq:
         line["decode_fast"] = dict(res.get("fast") or {}, quantizer=fq,
