@@ -632,7 +632,10 @@ def _ref_model_file(c, d):
     blob = bh.synth_model(c["vocab"], c["d_model"], c["n_layers"], c["n_heads"], c["seed"],
                           c["dist"])
     path = os.path.join(d, "model_%d.bin" % c["d_model"])
-    blob.tofile(path)
+    with open(path, "wb") as f:
+        blob.tofile(f)
+        f.flush()
+        os.fsync(f.fileno())  # written back before a spinning pool starts
     return path
 
 

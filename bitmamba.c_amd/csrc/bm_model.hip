@@ -257,6 +257,11 @@ __global__ void k_advance_pos(int* ctl, int n) {
   if (threadIdx.x == 0 && blockIdx.x == 0) ctl[CTL_POS] = (ctl[CTL_POS] + n) % 3;
 }
 
+// a decode run's steps count from 0 (the tokens buffer is filled from its start)
+__global__ void k_restart_steps(int* ctl) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) ctl[CTL_STEP] = 0;
+}
+
 // x[t] = embed[tok[t]]; out-of-range ids read row 0 (src/model.c:1116-1122)
 __global__ void k_embed(const float* __restrict__ embed, int dm, int vocab,
                         const int* __restrict__ toks, float* __restrict__ x) {
@@ -1075,11 +1080,9 @@ extern "C" int bm_hip_model_decode(bm_hip_model_t* m, int n_steps, float penalty
   // continues from the current device state (token, history, position)
   if (ensure_out(m, n_steps > 0 ? n_steps : 1)) return -1;
   if (ensure_graph(m, penalty, true)) return -1;
-  int ctl[bm::CTL_WORDS];
-  MCHECK(hipMemcpyAsync(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost, m->stream));
-  MCHECK(hipStreamSynchronize(m->stream));
-  ctl[bm::CTL_STEP] = 0;
-  MCHECK(hipMemcpyAsync(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice, m->stream));
+  // on the device, in stream order: no host copy of the control words
+  hipLaunchKernelGGL(bm::k_restart_steps, dim3(1), dim3(64), 0, m->stream, m->ctl);
+  MCHECK(hipGetLastError());
   return run_steps(m, n_steps, decode_ms);
 }
 

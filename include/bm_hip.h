@@ -407,7 +407,13 @@ int bm_hip_model_layer_state(const bm_hip_model_t *m,
  * prompt[n-1], each step one replay of a captured hipGraph with no host
  * synchronization.  Writes the tokens; *decode_ms = device time of the
  * steps (prefill excluded, as the reference's tok/s).  Returns the number of
- * tokens (cut after the first 50256 or 0 when stop_on_eos), -1 on error. */
+ * tokens (cut after the first 50256 or 0 when stop_on_eos), -1 on error.
+ * stop_on_eos only cuts the returned list: all n_steps steps run on the
+ * device, so the recurrent state, ring position, history, logits and
+ * sampler state are left n_steps past the prompt, where the reference's
+ * loop (src/main.c:498) stops stepping at the end token.  A caller that
+ * continues after an end token restarts from its own state (reset +
+ * prefill, or bm_hip_model_state_load). */
 int bm_hip_model_generate(bm_hip_model_t *m,
                           const int32_t *prompt,
                           int n_prompt,
