@@ -337,8 +337,8 @@ def leg_gemv1(L, reps=200):
                     "in cache between calls); drop-in = hip_bitlinear_forward on host buffers, "
                     "weights uploaded per call (not in a registered image); drop-in registered "
                     "= the same entry on a model image registered by bm_hip_set_mmap "
-                    "(K=1024 -> N=4192), per call: x up, quantize + GEMV, results down, one "
-                    "synchronisation")
+                    "(K=1024 -> N=4192), per call: one kernel reading x from and writing its "
+                    "results to mapped host memory, completion polled by the host")
     res.update(cpu_gemv1())
     return res
 
