@@ -106,6 +106,7 @@ SIGNATURES = {
     "bm_hip_model_state_load": (_i, [_vp, _vp, _sz]),
     "bm_hip_model_logits": (_i, [_vp, _vp]),
     "bm_hip_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
+    "bm_hip_model_set_layer_state": (_i, [_vp, _i, _vp, _vp, _i]),
     "bm_hip_model_generate": (_i, [_vp, _vp, _i, _i, _f, _i, _vp, C.POINTER(C.c_double)]),
     "bm_hip_model_decode": (_i, [_vp, _i, _f, C.POINTER(C.c_double)]),
     "bm_hip_model_tokens": (_i, [_vp, _vp, _i]),

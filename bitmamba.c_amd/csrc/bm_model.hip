@@ -1050,6 +1050,24 @@ extern "C" int bm_hip_model_layer_state(const bm_hip_model_t* m, int layer, floa
   return ctl[bm::CTL_POS];
 }
 
+extern "C" int bm_hip_model_set_layer_state(bm_hip_model_t* m, int layer, const float* conv_state,
+                                            const float* ssm_state, int conv_pos) {
+  if (layer < 0 || layer >= m->nl || conv_pos < 0 || conv_pos > 2 || !conv_state || !ssm_state) {
+    bm_set_error("set_layer_state: invalid arguments (layer=%d conv_pos=%d)", layer, conv_pos);
+    return -1;
+  }
+  MCHECK(hipStreamSynchronize(m->stream));
+  MCHECK(hipMemcpy(m->conv_state + (size_t)layer * 3 * m->di, conv_state, (size_t)3 * m->di * 4,
+                   hipMemcpyHostToDevice));
+  MCHECK(hipMemcpy(m->ssm_state + (size_t)layer * m->di, ssm_state, (size_t)m->di * 4,
+                   hipMemcpyHostToDevice));
+  int ctl[bm::CTL_WORDS];
+  MCHECK(hipMemcpy(ctl, m->ctl, sizeof(ctl), hipMemcpyDeviceToHost));
+  ctl[bm::CTL_POS] = conv_pos;
+  MCHECK(hipMemcpy(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice));
+  return 0;
+}
+
 extern "C" int bm_hip_model_generate(bm_hip_model_t* m, const int32_t* prompt, int n_prompt,
                                      int n_steps, float penalty, int stop_on_eos,
                                      int32_t* out_tokens, double* decode_ms) {

@@ -401,6 +401,18 @@ int bm_hip_model_layer_state(const bm_hip_model_t *m,
                              int layer,
                              float *conv_state,
                              float *ssm_state);
+/* The inverse: one layer's conv ring [3][d_inner], ssm state [d_inner] and
+ * ring position (the block cache fields of src/bitmamba.h:84-87) into the
+ * device model.  The device keeps one ring position for all layers, as the
+ * reference's layers advance together.  With bm_hip_model_layer_state this
+ * is the prefill hook for model_prefill (the Metal spot, src/model.c:
+ * 1050-1055): push the blocks' state, bm_hip_model_prefill, pull it back.
+ * 0, or -1 with bm_hip_last_error(). */
+int bm_hip_model_set_layer_state(bm_hip_model_t *m,
+                                 int layer,
+                                 const float *conv_state,
+                                 const float *ssm_state,
+                                 int conv_pos);
 /* The decode loop of src/main.c:443-500 on the device: prefill
  * prompt[0..n-2], history = prompt, then n_steps steps (greedy or sampled,
  * bm_hip_model_set_sampler) from

@@ -259,6 +259,21 @@ int bmref_model_layer_state(void *h,
     return b->conv_pos;
 }
 
+/* the inverse of bmref_model_layer_state */
+void bmref_model_set_layer_state(void *h,
+                                 int layer,
+                                 const float *conv_state,
+                                 const float *ssm_state,
+                                 int conv_pos)
+{
+    bitmamba_model_t *m = (bitmamba_model_t *) h;
+    bitmamba_block_t *b = &m->layers[layer];
+    memcpy(b->conv_state, conv_state,
+           (size_t) (b->d_conv - 1) * b->d_inner * sizeof(float));
+    memcpy(b->ssm_state, ssm_state, (size_t) b->d_inner * sizeof(float));
+    b->conv_pos = conv_pos;
+}
+
 /* ---------------------------------------------------------------------------
  * The HIP backend wired into this build's own plugin table, as a reference
  * tree built with HAS_HIP would do it (the table's types must agree): the

@@ -79,6 +79,7 @@ _REF_SIGS = {
     "bmref_model_vocab": (_i, [_vp]),
     "bmref_model_layer_state": (_i, [_vp, _i, _vp, _vp]),
     "bmref_use_hip": (_i, [_vp]),
+    "bmref_model_set_layer_state": (None, [_vp, _i, _vp, _vp, _i]),
     "bmref_kernels_name": (C.c_char_p, []),
     "bmref_model_image": (_i, [_vp, C.POINTER(_vp), C.POINTER(_sz)]),
 }
