@@ -227,6 +227,53 @@ def test_stress_m4096_sampled_and_linear(hip):
     np.testing.assert_array_equal(ga + gb, got[:256])
 
 
+def test_stress_m4096_full_exact(hip):
+    """M=4096 at full size, every one of the 4096 x 8192 int32 totals against
+    the brute-force product Σ x·decode(W) (float32 BLAS is exact here: every
+    partial sum is an integer below 127 · 8192 < 2^24)."""
+    K = N = 8192
+    M = 4096
+    note("stress M=4096 full")
+    packed = bh.synth_ternary(5, 1, N, K, bh.SYNTH_P0_60)
+    xq = bh.synth_int8(5, 3, (M, K))
+    got = gpu_gemm_i32(hip, xq, packed, N, K, canonical=1)
+    w = native.decode_dense(packed, K).astype(np.float32)
+    expect = xq.astype(np.float32) @ w.T
+    np.testing.assert_array_equal(got, expect.astype(np.int32))
+
+
+def _epilogue_ref(xq, sc, packed, N, K, w_scale):
+    """The fp32 outputs of src/kernel.c:388-428 from exact slice totals:
+    out = 0; out += (float)total_s * inv per 1024-column slice in order,
+    inv = 1/(scale_x * w_scale); totals by float32 BLAS (exact: below 2^24)."""
+    f = np.float32
+    w = native.decode_dense(packed, K).astype(f)
+    x = xq.astype(f)
+    inv = f(1.0) / (sc.astype(f) * f(w_scale))
+    out = np.zeros((x.shape[0], N), f)
+    for s0 in range(0, K, 1024):
+        t = x[:, s0:s0 + 1024] @ w[:, s0:s0 + 1024].T
+        out = (out + (t.astype(f) * inv[:, None]).astype(f)).astype(f)
+    return out
+
+
+def test_prefill_full_exact(hip):
+    """The two M=2048 prefill products at full size: every int8 activation
+    against the oracle's quantizer and every fp32 output against the
+    reference's slice epilogue on brute-force totals."""
+    r = rnd(4096)
+    for M, K, N, seed in ((2048, 2048, 8512, 11), (2048, 4096, 2048, 12)):
+        note("prefill full M=%d K=%d N=%d" % (M, K, N))
+        packed = bh.synth_ternary(seed, 1, N, K, bh.SYNTH_UNIFORM)
+        x = bh.synth_normal(seed, 2, (M, K), 1.0)
+        x[r.random((M, K)) < 0.01] *= 10.0
+        g = np.ones(K, np.float32)
+        out, xq = gpu_bitlinear(hip, x, packed, N, K, 0.02, g, canonical=1)
+        _, oq, osc, _ = native.orc_quantize_rows(x, g)
+        np.testing.assert_array_equal(xq, oq)
+        same_bits(out, _epilogue_ref(oq, osc, packed, N, K, 0.02), "out")
+
+
 # ------------------------------------------------------------ fp32 BitLinear
 FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257),
              (3, 1024, 300), (1, 1000, 77), (2, 1026, 33), (1, 100, 10),
