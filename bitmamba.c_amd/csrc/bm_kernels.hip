@@ -807,7 +807,7 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
                                                  const float* __restrict__ scale_x, int M,
                                                  const uint8_t* __restrict__ W, int N, int K,
                                                  float w_scale, float* __restrict__ out,
-                                                 int32_t* __restrict__ out_i32) {
+                                                 int32_t* __restrict__ out_i32, int ldo) {
   constexpr bool I32 = MODE == 2;
   constexpr int GBN = 64 * WN, NT = 128 * WN;  // tile columns, threads
   constexpr int TBM = 64 * MT;                // tile rows
@@ -989,10 +989,10 @@ __global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict_
         const int r = m0 + wm * 32 * MT + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (r < M && n < N) {
           if (I32)
-            out_i32[(size_t)r * N + n] = __float_as_int(o[mt][nt][v]);
+            out_i32[(size_t)r * ldo + n] = __float_as_int(o[mt][nt][v]);
           else
-            out[(size_t)r * N + n] =
-                MODE == 1 ? __fadd_rn(out[(size_t)r * N + n], o[mt][nt][v]) : o[mt][nt][v];
+            out[(size_t)r * ldo + n] =
+                MODE == 1 ? __fadd_rn(out[(size_t)r * ldo + n], o[mt][nt][v]) : o[mt][nt][v];
         }
       }
     }
@@ -1118,36 +1118,75 @@ static double rounds_cost(long long tiles, int slots, bool two_per_cu) {
   return (double)full + (rest == 0 ? 0.0 : (two_per_cu && rest <= slots / 2) ? 0.6 : 1.0);
 }
 enum { GEMM_64x128 = 0, GEMM_128x128 = 1, GEMM_128x256 = 2 };
-static int gemm_shape(int M, int N) {
+static int gemm_shape(int M, int N, double* cost = nullptr) {
   const long long tn128 = (N + 127) / 128, tn256 = (N + 255) / 256;
   const double c64 = 0.58 * rounds_cost((M + 63) / 64 * tn128, 2 * kCUs, true);
   const double c128 = rounds_cost((M + 127) / 128 * tn128, 2 * kCUs, true);
   const double c256 = 0.85 * rounds_cost((M + 127) / 128 * tn256, kCUs, false);
-  if (c256 <= c128 && c256 <= c64) return GEMM_128x256;
-  return c64 < c128 ? GEMM_64x128 : GEMM_128x128;
+  int shape = c64 < c128 ? GEMM_64x128 : GEMM_128x128;
+  double c = c64 < c128 ? c64 : c128;
+  if (c256 <= c) {
+    shape = GEMM_128x256;
+    c = c256;
+  }
+  if (cost) *cost = c;
+  return shape;
+}
+// Columns of a first launch that leaves the rest of N to a second one (a
+// multiple of 256), or N for a single launch.  Two launches pay when the
+// tiles of the whole product end in a nearly empty round: M=2048,
+// K=2048 -> 8512 is 3 rounds of 544 tiles of 128 x 256 (65.3 us), but 8192
+// columns are exactly 2 rounds (48.5 us) and the other 320 take 9.9 us as
+// 64 x 128 tiles.  A second launch is charged 0.1 round.
+static int gemm_split(int M, int N) {
+  double best;
+  gemm_shape(M, N, &best);
+  best -= 0.1;
+  int split = N;
+  for (int head = (N - 1) / 256 * 256; head > 0; head -= 256) {  // ties: the larger head
+    double a, b;
+    gemm_shape(M, head, &a);
+    gemm_shape(M, N - head, &b);
+    if (a + b < best) {
+      best = a + b;
+      split = head;
+    }
+  }
+  return split;
 }
 
 template <bool CANON, int MODE>
-static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
-                         int K, float w_scale, void* out, hipStream_t s) {
+static hipError_t gemm_launch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
+                              int N, int K, float w_scale, void* out, int ldo, hipStream_t s) {
   const int shape = gemm_shape(M, N);
   if (shape == GEMM_128x256) {
     const dim3 grid((unsigned)((M + 127) / 128 * ((N + 255) / 256)));
     hipLaunchKernelGGL((k_gemm<CANON, MODE, 4, 2>), grid, dim3(512), 0, s, act,
                        act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
-                       (int32_t*)out);
+                       (int32_t*)out, ldo);
   } else if (shape == GEMM_64x128) {
     const dim3 grid((unsigned)((M + 63) / 64 * ((N + 127) / 128)));
     hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 1>), grid, dim3(256), 0, s, act,
                        act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
-                       (int32_t*)out);
+                       (int32_t*)out, ldo);
   } else {
     const dim3 grid((unsigned)((M + 127) / 128 * ((N + 127) / 128)));
     hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 2>), grid, dim3(256), 0, s, act,
                        act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
-                       (int32_t*)out);
+                       (int32_t*)out, ldo);
   }
   return hipGetLastError();
+}
+
+template <bool CANON, int MODE>
+static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
+                         int K, float w_scale, void* out, hipStream_t s) {
+  const int head = gemm_split(M, N);
+  hipError_t e = gemm_launch<CANON, MODE>(act, scale_x, M, W, head, K, w_scale, out, N, s);
+  if (e != hipSuccess || head == N) return e;
+  // the last N % 256 columns: their weight rows and output columns
+  return gemm_launch<CANON, MODE>(act, scale_x, M, W + (size_t)head * (K / 4), N - head, K,
+                                  w_scale, (uint8_t*)out + 4 * (size_t)head, N, s);
 }
 
 // which kernel serves a product of this shape
