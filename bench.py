@@ -35,6 +35,9 @@ Prints ONE JSON line.  Legs (all by default):
   d255m     255M-shape greedy decode, 128 steps (tok/s, stream identity)
   stress    int8-input ternary products at K = N = 8192, p(0) = 0.6, exact
             int32 outputs: M = 1, 16 (weight GB/s, warm) and 4096 (TOP/s)
+  vendor    the vendor library's dense int8 GEMM (torch._int_mm on hipBLASLt)
+            at the prefill and stress shapes: a reference point without the
+            ternary decode or the fp32 epilogue
   mfma      the int8 MFMA ceiling: 2 waves per SIMD of back-to-back
             v_mfma_i32_32x32x32_i8, fixed operands and then hashed int8
             activations against codes 0..2 (the GEMM's data; the sustained
@@ -638,6 +641,61 @@ def leg_prefill(L, reps=10):
     return out
 
 
+def leg_vendor(timeout_s=180):
+    """The vendor library's dense int8 GEMM (torch._int_mm, which runs on
+    hipBLASLt) on the prefill and stress shapes: int8 x int8 -> int32 with
+    neither the ternary decode nor the fp32 slice epilogue -- a reference
+    point for what an int8 MFMA GEMM reaches at these sizes on this GPU.
+    Run in a child process of its own (torch does not see the device in a
+    process whose HIP runtime this library already started)."""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-child"],
+                           stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                           timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        log("vendor int8 GEMM child timed out")
+        return None
+    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+    if r.returncode != 0 or not lines:
+        log("vendor int8 GEMM child failed (rc %d): %s" % (r.returncode, r.stderr[-300:]))
+        return None
+    return json.loads(lines[-1])
+
+
+def vendor_child(reps=20):
+    try:
+        import torch
+    except ImportError:
+        print("{}")
+        return
+    if not torch.cuda.is_available():
+        print("{}")
+        return
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for M, K, N in ((2048, 2048, 8512), (2048, 4096, 2048), (4096, 8192, 8192)):
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+        b = torch.randint(-1, 2, (N, K), dtype=torch.int8, device="cuda", generator=g)
+        bt = b.t()  # K x N, column-major: the layout hipBLASLt takes without a copy
+        for _ in range(3):
+            torch._int_mm(a, bt)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch._int_mm(a, bt)
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        out["%dx%dx%d" % (M, K, N)] = dict(us=round(us, 1), tops=round(tops, 1),
+                                           frac=round(tops / I8_PEAK_TOPS, 4))
+        del a, b, bt
+    out["note"] = ("torch._int_mm (hipBLASLt), dense int8 operands, int32 out; no ternary decode, "
+                   "no fp32 epilogue")
+    print(json.dumps(out), flush=True)
+
+
 def cpu_threads():
     try:
         allowed = len(os.sched_getaffinity(0))
@@ -862,6 +920,9 @@ def main():
     if len(sys.argv) == 4 and sys.argv[1] == "--cpu-child":
         cpu_child(int(sys.argv[2]), float(sys.argv[3]))
         return
+    if len(sys.argv) == 2 and sys.argv[1] == "--vendor-child":
+        vendor_child()
+        return
     if len(sys.argv) == 4 and sys.argv[1] == "--cpu-gemv":
         cpu_gemv_child(int(sys.argv[2]), int(sys.argv[3]))
         return
@@ -870,7 +931,8 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--legs",
-                    default="decode,sampled,fast,roofline,mfma,prefill,d255m,gemv1,stress,cpu")
+                    default="decode,sampled,fast,roofline,mfma,prefill,d255m,gemv1,stress,vendor,"
+                            "cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: the BitLinear hot path runs on exactly one GPU (there is no "
@@ -938,6 +1000,9 @@ def main():
     strs = leg_stress(L) if "stress" in legs else None
     if strs:
         log("stress K=N=8192: %s" % json.dumps(strs))
+    vend = leg_vendor() if "vendor" in legs else None
+    if vend:
+        log("vendor int8 GEMM: %s" % json.dumps(vend))
     cpy = leg_copy(L) if "copy" in legs else None
     if cpy:
         log("copy: %s" % json.dumps(cpy))
@@ -988,6 +1053,7 @@ def main():
     line["decode_255m"] = d255
     line["bitlinear_k1024_n4384"] = g1
     line["stress_k8192_n8192"] = strs
+    line["vendor_int8_gemm"] = vend
     line["cpu_baseline"] = cpu
     if cpy:
         line["copy_calibration"] = cpy
