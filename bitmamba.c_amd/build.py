@@ -17,8 +17,11 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
-    # parity: no a*b+c contraction anywhere in the device code, and fp32
-    # division as the correctly rounded IEEE sequence
+    # parity: no a*b+c contraction anywhere in the device code; the device
+    # code divides and takes square roots only through bm_fp.h, which spells
+    # out the correctly rounded sequences (the option below is the compiler's
+    # default and only matters for a plain `/` or sqrtf, of which there are
+    # none; tests/test_fp_build.py checks the equivalence)
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     # packed fp32 instructions off (wrong results seen on this hardware)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
