@@ -1135,13 +1135,15 @@ static int gemm_shape(int M, int N, double* cost = nullptr) {
 // Columns of a first launch that leaves the rest of N to a second one (a
 // multiple of 256), or N for a single launch.  Two launches pay when the
 // tiles of the whole product end in a nearly empty round: M=2048,
-// K=2048 -> 8512 is 3 rounds of 544 tiles of 128 x 256 (65.3 us), but 8192
-// columns are exactly 2 rounds (48.5 us) and the other 320 take 9.9 us as
-// 64 x 128 tiles.  A second launch is charged 0.1 round.
+// K=2048 -> 8512 is 3 rounds of 544 tiles of 128 x 256 (65.8 us), but 8192
+// columns are exactly 2 rounds (46.8 us) and the other 320 take 10.9 us as
+// 64 x 128 tiles.  The second launch is charged 0.45 round beyond its own
+// estimate (its launch and latency): less made M=1024 -> 8384 and
+// M=1233 -> 8512 split and run 1.5-2 us slower than one launch.
 static int gemm_split(int M, int N) {
   double best;
   gemm_shape(M, N, &best);
-  best -= 0.1;
+  best -= 0.45;
   int split = N;
   for (int head = (N - 1) / 256 * 256; head > 0; head -= 256) {  // ties: the larger head
     double a, b;
