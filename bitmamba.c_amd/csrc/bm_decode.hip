@@ -234,31 +234,29 @@ __device__ float pro_quant(const float4 (&xv)[C], const float4 (&gv)[C], float r
 }
 
 // ---------------------------------------------------------------------------
-// Prologue for K = 1024 * G (G in {1, 2, 4}): thread t owns the 16-column
-// group t (t < K/16) in registers for the whole prologue; the squares go
-// through LDS once to reach the chain layout, wave 0 runs the chains, and
-// the int8 values are packed straight from registers.  Group t lies in
-// slice t/64 = the thread's wave.  Returns scale_x.
+// Prologue for K = 1024 * G (G in {1, 2, 4}): every thread of the block owns
+// 4G consecutive columns (float4s G*t .. G*t+G-1) in registers for the whole
+// prologue, so all four waves share the scaling and packing work whatever K
+// is; the R = 4/G threads of a 16-column group sit in consecutive lanes.
+// The squares go through LDS once to reach the chain layout, wave 0 runs the
+// chains, and the int8 values are packed straight from registers.  Returns
+// scale_x.
 //   PRENORM: x first becomes (x * rms(x)) * g_pre (the final norm).
 // ---------------------------------------------------------------------------
 template <int G>
-__device__ __forceinline__ void put_squares(const float4 (&v)[4], bool has, const Lds& l) {
+__device__ __forceinline__ void put_squares(const float4 (&v)[G], const Lds& l) {
   constexpr int E = 1024 * G / 64;
-  if (!has) return;
-  // column 16t + 4k + j is element 4t + k of chain j (segments of E
-  // elements padded by 4 floats)
-  const int e = 4 * (int)threadIdx.x;
+  // column 4e + j is element e of chain j (segments of E elements padded by
+  // 4 floats); the thread's elements G*t .. G*t+G-1 lie in one segment
+  const int e = G * (int)threadIdx.x;
   const int pe = e + 4 * (e / E);
-  *(float4*)&l.sq[pe] = make_float4(__fmul_rn(v[0].x, v[0].x), __fmul_rn(v[1].x, v[1].x),
-                                    __fmul_rn(v[2].x, v[2].x), __fmul_rn(v[3].x, v[3].x));
-  *(float4*)&l.sq[l.stride + pe] = make_float4(__fmul_rn(v[0].y, v[0].y), __fmul_rn(v[1].y, v[1].y),
-                                               __fmul_rn(v[2].y, v[2].y), __fmul_rn(v[3].y, v[3].y));
-  *(float4*)&l.sq[2 * l.stride + pe] =
-      make_float4(__fmul_rn(v[0].z, v[0].z), __fmul_rn(v[1].z, v[1].z), __fmul_rn(v[2].z, v[2].z),
-                  __fmul_rn(v[3].z, v[3].z));
-  *(float4*)&l.sq[3 * l.stride + pe] =
-      make_float4(__fmul_rn(v[0].w, v[0].w), __fmul_rn(v[1].w, v[1].w), __fmul_rn(v[2].w, v[2].w),
-                  __fmul_rn(v[3].w, v[3].w));
+#pragma unroll
+  for (int k = 0; k < G; ++k) {
+    l.sq[pe + k] = __fmul_rn(v[k].x, v[k].x);
+    l.sq[l.stride + pe + k] = __fmul_rn(v[k].y, v[k].y);
+    l.sq[2 * l.stride + pe + k] = __fmul_rn(v[k].z, v[k].z);
+    l.sq[3 * l.stride + pe + k] = __fmul_rn(v[k].w, v[k].w);
+  }
 }
 
 // rms = 1/sqrtf(sum/K + 1e-6f) from the squares in LDS; wave 0 runs the
@@ -289,119 +287,161 @@ __device__ __forceinline__ float chain_rms(const Lds& l, F&& idle = NoWork{}) {
   return l.bc[0];
 }
 
-// the thread's 16-column group of the input and of the norm weights, loaded
-// at kernel entry (before the weight rows, so that the prologue's first
-// wait covers these loads only)
-template <bool PRENORM>
+// the thread's columns of the input and of the norm weights, loaded at
+// kernel entry (before the weight rows, so that the prologue's first wait
+// covers these loads only)
+template <int G, bool PRENORM>
 struct SplitIn {
-  float4 xv[4], gv[4], gp[PRENORM ? 4 : 1];
+  float4 xv[G], gv[G], gp[PRENORM ? G : 1];
 };
 
 template <int G, bool PRENORM>
-__device__ __forceinline__ void split_load(SplitIn<PRENORM>& in, const float* __restrict__ x,
+__device__ __forceinline__ void split_load(SplitIn<G, PRENORM>& in, const float* __restrict__ x,
                                            const float* __restrict__ g_pre,
                                            const float* __restrict__ g) {
-  constexpr int NG = 1024 * G / 16;
-  const int c4 = 4 * ((int)threadIdx.x < NG ? (int)threadIdx.x : 0);
+  const int c4 = G * (int)threadIdx.x;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < G; ++k) {
     in.xv[k] = ((const float4*)x)[c4 + k];
     in.gv[k] = ((const float4*)g)[c4 + k];
     if constexpr (PRENORM) in.gp[k] = ((const float4*)g_pre)[c4 + k];
   }
 }
 
-// fast mode: 1/rms from the pairwise tree (one block barrier)
+// fast mode: 1/rms from the pairwise tree (one block barrier).  A 16-column
+// leaf is ((q0 + q1) + (q2 + q3)) over its four float4s; the thread holds G
+// of them, and the first butterfly steps of the wave tree finish the leaf
+// across its R = 4/G lanes, the rest pair the leaves in index order.
 template <int G>
-__device__ __forceinline__ float fast_rms(const float4 (&xv)[4], bool has, const Lds& l) {
+__device__ __forceinline__ float fast_rms(const float4 (&xv)[G], const Lds& l) {
   constexpr int K = 1024 * G;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float w = wave_tree_f32(has ? sq_tree16(xv) : 0.0f);
-  if (lane == 0 && wave < G) l.bc[12 + wave] = w;
+  float t[G];
+#pragma unroll
+  for (int k = 0; k < G; ++k)
+    t[k] = __fadd_rn(__fadd_rn(__fmul_rn(xv[k].x, xv[k].x), __fmul_rn(xv[k].y, xv[k].y)),
+                     __fadd_rn(__fmul_rn(xv[k].z, xv[k].z), __fmul_rn(xv[k].w, xv[k].w)));
+  float part;
+  if constexpr (G == 4)
+    part = __fadd_rn(__fadd_rn(t[0], t[1]), __fadd_rn(t[2], t[3]));
+  else if constexpr (G == 2)
+    part = __fadd_rn(t[0], t[1]);
+  else
+    part = t[0];
+  const float w = wave_tree_f32(part);
+  if (lane == 0) l.bc[12 + wave] = w;
   __syncthreads();
-  const float s = tree_top<G>(l.bc + 12);
+  const float s = tree_top<4>(l.bc + 12);
   return cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(s, 1.0f / K), 1e-6f)));
 }
 
 // idle: work for waves 1.. while wave 0 runs the first chain (the first
 // fast-mode tree has no such window: they run it at once)
 template <int G, bool PRENORM, typename F = NoWork>
-__device__ float split_prologue(SplitIn<PRENORM>& in, const Lds& l, bool fast,
+__device__ float split_prologue(SplitIn<G, PRENORM>& in, const Lds& l, bool fast,
                                 float* __restrict__ xn_out = nullptr,
                                 int8_t* __restrict__ xq_out = nullptr, F&& idle = NoWork{}) {
-  constexpr int NG = 1024 * G / 16;
+  constexpr int R = 4 / G, CPT = 4 * G;  // threads per 16-column group, columns per thread
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool has = tid < NG;
-  const int c4 = 4 * (has ? tid : 0);
-  float4 (&xv)[4] = in.xv;
-  const float4 (&gv)[4] = in.gv;
-  const float4 (&gp)[PRENORM ? 4 : 1] = in.gp;
+  const int c4 = G * tid;
+  float4 (&xv)[G] = in.xv;
+  const float4 (&gv)[G] = in.gv;
+  const float4 (&gp)[PRENORM ? G : 1] = in.gp;
+  // slice sums are accumulated from R waves each: cleared before the first
+  // barrier below
+  if (R > 1 && tid < G) l.slices[tid] = 0;
   float rms;
   if (fast) {
     if (threadIdx.x >= 64) idle();
-    rms = fast_rms<G>(xv, has, l);
+    rms = fast_rms<G>(xv, l);
   } else {
-    put_squares<G>(xv, has, l);
+    put_squares<G>(xv, l);
     rms = chain_rms<G>(l, idle);
   }
   if constexpr (PRENORM) {
     // final_feat = (x * rms) * norm_f (src/model.c:1225, src/kernel.c:93-103)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) xv[k] = scale4(xv[k], rms, gp[k]);
+    for (int k = 0; k < G; ++k) xv[k] = scale4(xv[k], rms, gp[k]);
     if (fast) {
       __syncthreads();  // the first tree's sums are read before they are replaced
-      rms = fast_rms<G>(xv, has, l);
+      rms = fast_rms<G>(xv, l);
     } else {
-      put_squares<G>(xv, has, l);
+      put_squares<G>(xv, l);
       rms = chain_rms<G>(l);
     }
   }
   // int8 quantization (src/kernel.c:93-128, 358-386)
   float mx = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < G; ++k) {
     xv[k] = scale4(xv[k], rms, gv[k]);
     mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[k].x), fabsf(xv[k].y)),
                          fmaxf(fabsf(xv[k].z), fabsf(xv[k].w))));
-    if (xn_out && has) ((float4*)xn_out)[c4 + k] = xv[k];
+    if (xn_out) ((float4*)xn_out)[c4 + k] = xv[k];
   }
-  mx = wave_max_f32(has ? mx : 0.0f);
+  mx = wave_max_f32(mx);
   if (lane == 0) l.bc[8 + wave] = mx;
   __syncthreads();
   const float max_abs = fmaxf(fmaxf(l.bc[8], l.bc[9]), fmaxf(l.bc[10], l.bc[11]));
   const float scale_x = cr_divf(127.0f, __fadd_rn(max_abs, 1e-5f));
+  int q[CPT];
   int qsum = 0;
-  if (has) {
-    int q[16];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float vv[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+  for (int k = 0; k < G; ++k) {
+    const float vv[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        q[4 * k + j] = (int)(int8_t)q8_of(vv[j], scale_x);
-        qsum += q[4 * k + j];
-      }
-    }
-    uint32_t le = 0, lo = 0, he = 0, ho = 0;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      le |= (uint32_t)(q[2 * n] & 15) << (4 * n);
-      lo |= (uint32_t)(q[2 * n + 1] & 15) << (4 * n);
-      he |= (uint32_t)((q[2 * n] >> 4) & 15) << (4 * n);
-      ho |= (uint32_t)((q[2 * n + 1] >> 4) & 15) << (4 * n);
-    }
-    *(uint4*)(l.nib + 4 * tid) = make_uint4(le, lo, he, ho);
-    if (xq_out) {
-      uint32_t b[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        b[k] = (uint32_t)(q[4 * k] & 255) | (uint32_t)(q[4 * k + 1] & 255) << 8 |
-               (uint32_t)(q[4 * k + 2] & 255) << 16 | (uint32_t)(q[4 * k + 3] & 255) << 24;
-      *(uint4*)(xq_out + 16 * tid) = make_uint4(b[0], b[1], b[2], b[3]);
+    for (int j = 0; j < 4; ++j) {
+      q[4 * k + j] = (int)(int8_t)q8_of(vv[j], scale_x);
+      qsum += q[4 * k + j];
     }
   }
-  const int ssum = wave_sum_i32(qsum);  // the wave's 64 groups = slice `wave`
-  if (lane == 0 && wave < G) l.slices[wave] = ssum;
+  // this thread's nibbles of its group's four split-nibble words: columns
+  // 2n (even) and 2n+1 (odd) of the group are nibble n; the thread's
+  // columns start at 16-column offset CPT * (tid % R)
+  const int n0 = (CPT / 2) * (tid % R);
+  uint32_t le = 0, lo = 0, he = 0, ho = 0;
+#pragma unroll
+  for (int n = 0; n < CPT / 2; ++n) {
+    const int sh = 4 * (n0 + n);
+    le |= (uint32_t)(q[2 * n] & 15) << sh;
+    lo |= (uint32_t)(q[2 * n + 1] & 15) << sh;
+    he |= (uint32_t)((q[2 * n] >> 4) & 15) << sh;
+    ho |= (uint32_t)((q[2 * n + 1] >> 4) & 15) << sh;
+  }
+  if constexpr (R >= 2) {  // the group's R lanes are adjacent: OR their parts
+    le |= (uint32_t)dpp_mov<0xB1>((int)le);
+    lo |= (uint32_t)dpp_mov<0xB1>((int)lo);
+    he |= (uint32_t)dpp_mov<0xB1>((int)he);
+    ho |= (uint32_t)dpp_mov<0xB1>((int)ho);
+  }
+  if constexpr (R == 4) {
+    le |= (uint32_t)dpp_mov<0x4E>((int)le);
+    lo |= (uint32_t)dpp_mov<0x4E>((int)lo);
+    he |= (uint32_t)dpp_mov<0x4E>((int)he);
+    ho |= (uint32_t)dpp_mov<0x4E>((int)ho);
+  }
+  if (tid % R == 0) *(uint4*)(l.nib + 4 * (tid / R)) = make_uint4(le, lo, he, ho);
+  if (xq_out) {
+    uint32_t b[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k)
+      b[k] = (uint32_t)(q[4 * k] & 255) | (uint32_t)(q[4 * k + 1] & 255) << 8 |
+             (uint32_t)(q[4 * k + 2] & 255) << 16 | (uint32_t)(q[4 * k + 3] & 255) << 24;
+    if constexpr (G == 4)
+      *(uint4*)(xq_out + CPT * tid) = make_uint4(b[0], b[1], b[2], b[3]);
+    else if constexpr (G == 2)
+      *(uint2*)(xq_out + CPT * tid) = make_uint2(b[0], b[1]);
+    else
+      *(uint32_t*)(xq_out + CPT * tid) = b[0];
+  }
+  // a 1024-column slice is R waves (wave w's columns are slice w / R)
+  const int ssum = wave_sum_i32(qsum);
+  if (lane == 0) {
+    if constexpr (R == 1)
+      l.slices[wave] = ssum;
+    else
+      atomicAdd(&l.slices[wave / R], ssum);
+  }
   __syncthreads();
   return scale_x;
 }
@@ -497,7 +537,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
 
   // the input vectors first (the prologue waits for them), then the weights
   float4 sx[WP ? 1 : C], sg[WP ? 1 : C], sg2[PRENORM && !WP ? C : 1];
-  SplitIn<PRENORM> sin;
+  SplitIn<C, PRENORM> sin;
   if constexpr (WP) {
     split_load<C, PRENORM>(sin, x, gamma_pre, gamma);
   } else {
@@ -716,7 +756,7 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   // input vector next (the prologue waits for it), then the weights
   const int pos = a.ctl[CTL_POS];
   float4 sx[WP ? 1 : C], sg[WP ? 1 : C];
-  SplitIn<false> sin;
+  SplitIn<C, false> sin;
   if constexpr (WP) {
     split_load<C, false>(sin, x, nullptr, gamma);
   } else {
