@@ -754,24 +754,29 @@ __global__ __launch_bounds__(256) void k_generic(const int8_t* __restrict__ xq, 
 
 // ---------------------------------------------------------------------------
 // Prefill / batched GEMM on int8 MFMA (v_mfma_i32_32x32x32_i8).
-//   block 256 threads = 2x2 waves, tile 128(M) x 128(N), each wave 64 x 64
-//   (2 x 2 MFMA tiles); K in stages of 128.
-//   Each stage (A: 128 rows x 128 permuted int8 activations; B: 128 weight
-//   rows x 32 packed bytes) is loaded into registers three stages ahead and
-//   written to one of three LDS buffers at the start of the stage before
-//   its use, so a load has two stages of MFMA work to arrive in and the
-//   LDS writes overlap the MFMAs; one barrier per stage.  LDS serves a
-//   16-byte read for 16 lanes per cycle from 64 banks: A's 16-byte chunks
-//   are XOR-swizzled by row/2 and B's two 16-byte halves by row/8, so the
-//   operand reads of 16 consecutive rows hit 16 different bank groups.
-//   B operands are decoded in registers: a lane's 16 packed bytes of one
-//   weight row are its operand for the stage's four 32-deep steps.
-//   Lane (j = lane%32, h = lane/32) covers columns kb + 64h + 16s.. in step
-//   s, for A and B alike.  Codes are used as is (0, 1, 2) and the slice sum
-//   of x is subtracted at each 1024-column slice boundary, where the int32
-//   totals are folded into fp32 in slice order.
+//   A block of WM x WN waves (WM = 2) owns a (32 MT WM) x (32 NTW WN)
+//   output tile; each wave MT x NTW MFMA tiles of 32 x 32.  K runs in stages
+//   of BK = 256 columns (128 when K is an odd multiple of 128) through an
+//   LDS ring of NBUF stages: A (the tile's rows of permuted int8
+//   activations) and B (the tile's weight rows, BK/4 packed bytes each) go
+//   straight from global memory into LDS (global_load_lds_dwordx4: each
+//   lane's 16 bytes land at the instruction's LDS base + 16 * lane, so the
+//   swizzle is applied to the global side), NBUF stages ahead of their use;
+//   each wave waits for its own loads of the next stage (vmcnt) and one
+//   barrier per stage publishes it.  Operands are read one 32-deep step
+//   ahead of their MFMAs, so the LDS latency hides behind the current
+//   step.  LDS serves a 16-byte read for 16 lanes per cycle from 64 banks:
+//   A's 16-byte chunks are XOR-swizzled by row (row/2 mod 8 for 8 chunks
+//   per row, row mod 16 for 16) and B's chunks by column, so the operand
+//   reads of 16 consecutive rows hit 16 different bank groups.
+//   Lane (j = lane%32, h = lane/32) covers columns kb + (BK/2) h + 16 s ..
+//   in step s, for A and B alike; its packed weight dword of step s decodes
+//   to the four int8 operand dwords (codes 0, 1, 2 as they are).  Each
+//   1024-column slice's accumulators start from -(slice sum of x) as the
+//   C operand of the slice's first MFMA (w = code - 1), and are folded into
+//   fp32 in slice order at its end (src/kernel.c:255-256, 407-425).
 // ---------------------------------------------------------------------------
-constexpr int GBM = 128, GBK = 128;  // largest tile rows and stage depth; columns: 64 * WN
+constexpr int GBK = 128;         // K granularity of the MFMA GEMM
 constexpr int GMAX_SLICES = 16;  // K <= 16384
 
 // Output tile of a block.  Workgroups go to the 8 XCDs round robin
@@ -791,202 +796,281 @@ __device__ __forceinline__ void gemm_tile_of(int b, int tiles_m, int tiles_n, in
   tn = r / rows;
 }
 
-template <int WN>
-struct GemmStage {
-  v4i a[8 / WN];  // A chunks of this thread
-  v4i b;          // 1 B chunk of this thread
-};
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16 bytes per lane from sbase + voff into LDS at lds_base + 16 * lane.
+// The compiler does not see the LDS write: completion is awaited with
+// wait_vm and published with a barrier.
+__device__ __forceinline__ void lds_load16(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(
+                   __builtin_amdgcn_readfirstlane(lds_base)),
+               "v"(voff), "s"(sbase));
+}
+// wait until at most N of this wave's vector memory operations are pending
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+template <int NCH>
+__device__ __forceinline__ int gemm_a_swz(int r) {
+  return NCH == 8 ? ((r >> 1) & 7) : (r & 15);
+}
+template <int NBC>
+__device__ __forceinline__ int gemm_b_swz(int n) {
+  return NBC == 2 ? ((n >> 3) & 1) : ((n >> 2) & 3);
+}
 
-// WN waves along N (2: 256 threads, tile 128 x 128, two blocks per CU;
-// 4: 512 threads, tile 128 x 256, one block per CU -- each A stage then
-// feeds twice the columns); MT 32-row MFMA tiles per wave along M (2: 128
-// tile rows; 1: 64, for grids that 128-row tiles leave short of the CUs)
-template <bool CANON, int MODE, int WN, int MT>
-__global__ __launch_bounds__(128 * WN, 2) void k_gemm(const uint8_t* __restrict__ act,
-                                                 size_t act_stride,
-                                                 const float* __restrict__ scale_x, int M,
-                                                 const uint8_t* __restrict__ W, int N, int K,
-                                                 float w_scale, float* __restrict__ out,
-                                                 int32_t* __restrict__ out_i32, int ldo) {
+template <bool CANON, int MODE, int MT, int NTW, int WN, int NBUF, int OCC, int BK>
+__global__ __launch_bounds__(128 * WN, OCC) void k_gemm(const uint8_t* __restrict__ act,
+                                                      size_t act_stride,
+                                                      const float* __restrict__ scale_x, int M,
+                                                      const uint8_t* __restrict__ W, int N, int K,
+                                                      float w_scale, float* __restrict__ out,
+                                                      int32_t* __restrict__ out_i32, int ldo) {
+  static_assert(BK == 128 || BK == 256, "stage depth");
   constexpr bool I32 = MODE == 2;
-  constexpr int GBN = 64 * WN, NT = 128 * WN;  // tile columns, threads
-  constexpr int TBM = 64 * MT;                // tile rows
-  constexpr int NA = 4 * MT / WN;             // A chunks per thread per stage
-  constexpr int BB = GBK / 4;                 // packed bytes per weight row per stage
-  __shared__ __attribute__((aligned(16))) uint8_t sA[3][TBM * GBK];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[3][GBN * BB];
-  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][TBM];
-  __shared__ __attribute__((aligned(16))) float s_inv[TBM];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+  constexpr int WM = 2, NW = WM * WN, NT = 64 * NW;
+  constexpr int BM = 32 * MT * WM, BN = 32 * NTW * WN;
+  constexpr int NCH = BK / 16, BB = BK / 4, NBC = BB / 16;  // A chunks per row; B bytes, chunks per column
+  constexpr int NQ = BK / 32;                                 // 32-deep steps per stage
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BB;
+  static_assert((A_BYTES / 16) % NT == 0 && (B_BYTES / 16) % NT == 0, "stage chunks per thread");
+  constexpr int NA = A_BYTES / 16 / NT, NB = B_BYTES / 16 / NT, PER = NA + NB;
+  constexpr int SPS = kSlice / BK;  // stages per slice
+  __shared__ __attribute__((aligned(16))) uint8_t sA[NBUF][A_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[NBUF][B_BYTES];
+  __shared__ __attribute__((aligned(16))) int s_sx[GMAX_SLICES][BM];
+  __shared__ __attribute__((aligned(16))) float s_inv[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / WN, wn = w % WN;
   const int j32 = lane & 31, h = lane >> 5;
   int tm, tn;
-  gemm_tile_of(blockIdx.x, (M + TBM - 1) / TBM, (N + GBN - 1) / GBN, tm, tn);
-  const int m0 = tm * TBM, n0 = tn * GBN;
+  gemm_tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
   const size_t wstride = (size_t)(K >> 2);
-  const size_t perm = act_perm_off(K);
-  const int n_slices = slices_of(K);
-  const int n_stages = K / GBK;
+  const int n_sl = slices_of(K);
+  const int n_st = K / BK;
+
+  // each thread's stage loads: LDS slot s = (i NW + w) 64 + lane of A
+  // (row s / NCH, position s % NCH) and of B (column s / NBC); rows and
+  // columns past M / N reload the last one
+  uint32_t a_off[NA], b_off[NB];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int s = (i * NW + w) * 64 + lane;
+    const int row = s / NCH, c = (s % NCH) ^ gemm_a_swz<NCH>(row);
+    a_off[i] = (uint32_t)((min(m0 + row, M - 1) - m0) * act_stride) + 16 * c;
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int s = (i * NW + w) * 64 + lane;
+    const int col = s / NBC, c = (s % NBC) ^ gemm_b_swz<NBC>(col);
+    b_off[i] = (uint32_t)((min(n0 + col, N - 1) - n0) * wstride) + 16 * c;
+  }
+  const uint8_t* a_base = act + (size_t)m0 * act_stride + act_perm_off(K);
+  const uint8_t* b_base = W + (size_t)n0 * wstride;
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const int buf = st % NBUF;
+    const uint8_t* ab = a_base + (size_t)st * BK;
+    const uint8_t* bb = b_base + (size_t)st * BB;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) lds_load16(ab, a_off[i], lds_addr(&sA[buf][(i * NW + w) * 1024]));
+#pragma unroll
+    for (int i = 0; i < NB; ++i) lds_load16(bb, b_off[i], lds_addr(&sB[buf][(i * NW + w) * 1024]));
+  };
 
   // per-row slice sums of x and 1/(scale_x * w_scale)
-  for (int i = tid; i < TBM * n_slices; i += NT) {
-    const int r = i % TBM, sl = i / TBM;
+  for (int i = tid; i < BM * n_sl; i += NT) {
+    const int r = i % BM, sl = i / BM;
     const int row = min(m0 + r, M - 1);
     s_sx[sl][r] = ((const int*)(act + (size_t)row * act_stride))[sl];
   }
-  if (tid < TBM) {
+  if (tid < BM) {
     const int row = min(m0 + tid, M - 1);
     s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[row], w_scale);
   }
 
-  // global -> registers: thread t loads A chunks g = t + NT*i (row g/8,
-  // chunk g%8) and B chunk t (weight row t/2, half t%2).  Rows past M / N
-  // reread the last one; stages past K reread the last stage.
-  auto load_stage = [&](int st, GemmStage<WN>& r) __attribute__((always_inline)) {
-    const int kb = min(st, n_stages - 1) * GBK;
+  v4i fa[2][MT];     // A operands of the current and the next step
+  uint4 fb[2][NTW];  // packed B of four steps
+  auto read_a = [&](int st, int q, v4i (&d)[MT]) __attribute__((always_inline)) {
+    const uint8_t* cA = sA[st % NBUF];
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int g = tid + NT * i;
-      const int row = min(m0 + (g >> 3), M - 1);
-      r.a[i] = *(const v4i*)(act + (size_t)row * act_stride + perm + kb + 16 * (g & 7));
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = (wm * MT + mt) * 32 + j32;
+      d[mt] = *(const v4i*)(cA + r * BK + 16 * (((NCH / 2) * h + q) ^ gemm_a_swz<NCH>(r)));
     }
-    const int n = min(n0 + (tid >> 1), N - 1);
-    r.b = *(const v4i*)(W + (size_t)n * wstride + (kb >> 2) + 16 * (tid & 1));
   };
-  auto store_stage = [&](int buf, const GemmStage<WN>& r) __attribute__((always_inline)) {
+  auto read_b = [&](int st, int u, uint4 (&d)[NTW]) __attribute__((always_inline)) {
+    const uint8_t* cB = sB[st % NBUF];
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int g = tid + NT * i;
-      const int row = g >> 3;
-      *(v4i*)(sA[buf] + row * GBK + 16 * ((g & 7) ^ ((row >> 1) & 7))) = r.a[i];
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int col = (wn * NTW + nt) * 32 + j32;
+      d[nt] = *(const uint4*)(cB + col * BB + 16 * (((NBC / 2) * h + u) ^ gemm_b_swz<NBC>(col)));
     }
-    const int col = tid >> 1;
-    *(v4i*)(sB[buf] + col * BB + 16 * ((tid & 1) ^ ((col >> 3) & 1))) = r.b;
   };
 
-  v16i acc[MT][2];
-  float o[MT][2][16];
+  v16i acc[MT][NTW];
+  float o[MT][NTW][16];
 #pragma unroll
   for (int a = 0; a < MT; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NTW; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         acc[a][b][v] = 0;
         o[a][b][v] = 0.0f;
       }
 
-  // one stage: X holds stage st+1 (loaded two stages ago) and goes to LDS
-  // first, so that the barrier closing the stage finds the writes long done;
-  // Y holds stage st+2 (in flight); Z is free and receives stage st+3
-  auto body = [&](int st, GemmStage<WN>& X, GemmStage<WN>& Y, GemmStage<WN>& Z)
-                  __attribute__((always_inline)) {
-    (void)Y;
-    store_stage((st + 1) % 3, X);  // the buffer stage st-2 used
-    const uint8_t* __restrict__ cA = sA[st % 3];
-    const uint8_t* __restrict__ cB = sB[st % 3];
-    v4i aop[MT][4];
+  // stages 0 .. NBUF-1 in flight, stage 0 published
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = wm * 32 * MT + mt * 32 + j32;
+  for (int i = 0; i < NBUF; ++i)
+    if (i < n_st) issue(i);
+  {
+    const int later = min(NBUF - 1, n_st - 1);
+    if (later >= 3) wait_vm<3 * PER>();
+    else if (later == 2) wait_vm<2 * PER>();
+    else if (later == 1) wait_vm<PER>();
+    else wait_vm<0>();
+  }
+  __syncthreads();
+  read_a(0, 0, fa[0]);
+  read_b(0, 0, fb[0]);
+
+  auto stage = [&](int st, auto pb_c) __attribute__((always_inline)) {
+    // NQ = 4: fb[PB] holds the stage's B and the next stage's goes to
+    // fb[PB ^ 1]; NQ = 8: fb[0] and fb[1] hold steps 0..3 and 4..7
+    constexpr int PB = NQ == 4 ? decltype(pb_c)::value : 0;
+    const bool first = I32 ? st == 0 : st % SPS == 0;
+    const int sl = st / SPS;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        aop[mt][q] = *(const v4i*)(cA + r * GBK + 16 * ((4 * h + q) ^ ((r >> 1) & 7)));
-    }
-    uint4 bw[2];
+    for (int q = 0; q < NQ; ++q) {
+      if (q < NQ - 1) {
+        read_a(st, q + 1, fa[(q + 1) & 1]);
+        if (NQ == 8 && q == 3) read_b(st, 1, fb[1]);
+      } else if (st + 1 < n_st) {
+        // publish stage st+1 (this wave's loads, then the barrier), refill
+        // the buffer of stage st, read the next stage's first operands
+        const int later = min(NBUF - 2, n_st - 2 - st);
+        if (later >= 2) wait_vm<2 * PER>();
+        else if (later == 1) wait_vm<PER>();
+        else wait_vm<0>();
+        __syncthreads();
+        if (st + NBUF < n_st) issue(st + NBUF);
+        read_a(st + 1, 0, fa[0]);
+        read_b(st + 1, 0, fb[NQ == 4 ? PB ^ 1 : 0]);
+      }
+      v4i bop[NTW];
+      const int cb = NQ == 4 ? PB : q / 4;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = wn * 64 + nt * 32 + j32;
-      bw[nt] = *(const uint4*)(cB + col * BB + 16 * (h ^ ((col >> 3) & 1)));
-    }
-    load_stage(st + 3, Z);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      v4i bop[2];
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const uint32_t w4[4] = {bw[nt].x, bw[nt].y, bw[nt].z, bw[nt].w};
-        const uint32_t pw = CANON ? w4[q] : canon_codes(w4[q]);
+      for (int nt = 0; nt < NTW; ++nt) {
+        const uint4 bw = fb[cb][nt];
+        const uint32_t w4[4] = {bw.x, bw.y, bw.z, bw.w};
+        const uint32_t pw = CANON ? w4[q & 3] : canon_codes(w4[q & 3]);
         bop[nt][0] = (int)(pw & 0x03030303u);
         bop[nt][1] = (int)((pw >> 2) & 0x03030303u);
         bop[nt][2] = (int)((pw >> 4) & 0x03030303u);
         bop[nt][3] = (int)((pw >> 6) & 0x03030303u);
       }
+      const v4i (&aq)[MT] = fa[q & 1];
+      if (q == 0 && first) {
+        // accumulators start at -(slice sum of x) of their rows (I32: of all slices)
+        v16i c[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] =
-              __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[mt][q], bop[nt], acc[mt][nt], 0, 0, 0);
+          for (int g = 0; g < 4; ++g) {
+            // rows 8g + 4h + (0..3) of the MFMA tile: elements 4g .. 4g+3
+            const int r0 = (wm * MT + mt) * 32 + 8 * g + 4 * h;
+            int4 sx4;
+            if (I32) {
+              sx4 = make_int4(0, 0, 0, 0);
+              for (int s2 = 0; s2 < n_sl; ++s2) {
+                const int4 t4 = *(const int4*)&s_sx[s2][r0];
+                sx4.x += t4.x;
+                sx4.y += t4.y;
+                sx4.z += t4.z;
+                sx4.w += t4.w;
+              }
+            } else {
+              sx4 = *(const int4*)&s_sx[sl][r0];
+            }
+            c[mt][4 * g + 0] = -sx4.x;
+            c[mt][4 * g + 1] = -sx4.y;
+            c[mt][4 * g + 2] = -sx4.z;
+            c[mt][4 * g + 3] = -sx4.w;
+          }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[mt], bop[nt], c[mt], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt)
+            acc[mt][nt] =
+                __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[mt], bop[nt], acc[mt][nt], 0, 0, 0);
+      }
     }
-
-    const int kb = st * GBK;
-    if (!I32 && (((kb + GBK) % kSlice == 0) || st + 1 == n_stages)) {
-      const int slice = kb / kSlice;
+    if (!I32 && (st % SPS == SPS - 1 || st + 1 == n_st)) {
+      // the slice's fp32 term, added in slice order (the first to 0)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
+        float inv[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          // rows 8g + 4h + (0..3) of the tile: acc elements v = 4g .. 4g+3
-          const int rb = wm * 32 * MT + mt * 32 + 8 * g + 4 * h;
-          const int4 sx4 = *(const int4*)&s_sx[slice][rb];
-          const float4 in4 = *(const float4*)&s_inv[rb];
-          const int sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
-          const float inv[4] = {in4.x, in4.y, in4.z, in4.w};
+          const float4 in4 = *(const float4*)&s_inv[(wm * MT + mt) * 32 + 8 * g + 4 * h];
+          inv[4 * g + 0] = in4.x;
+          inv[4 * g + 1] = in4.y;
+          inv[4 * g + 2] = in4.z;
+          inv[4 * g + 3] = in4.w;
+        }
+        if (sl == 0) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
+          for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              const int v = 4 * g + e;
-              o[mt][nt][v] =
-                  __fadd_rn(o[mt][nt][v], __fmul_rn((float)(acc[mt][nt][v] - sx[e]), inv[e]));
-              acc[mt][nt][v] = 0;
-            }
+            for (int v = 0; v < 16; ++v)
+              o[mt][nt][v] = __fadd_rn(0.0f, __fmul_rn((float)acc[mt][nt][v], inv[v]));
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              o[mt][nt][v] = __fadd_rn(o[mt][nt][v], __fmul_rn((float)acc[mt][nt][v], inv[v]));
         }
       }
     }
-    __syncthreads();
   };
 
-  GemmStage<WN> R0, R1, R2;
-  load_stage(0, R0);
-  load_stage(1, R1);
-  load_stage(2, R2);
-  store_stage(0, R0);
-  __syncthreads();
-  // three stages per turn so that each register set keeps its registers (no
-  // mid-turn exit: a merge there makes the loop head wait for every load)
   int st = 0;
-  for (; st + 3 <= n_stages; st += 3) {
-    body(st, R1, R2, R0);
-    body(st + 1, R2, R0, R1);
-    body(st + 2, R0, R1, R2);
+  for (; st + 2 <= n_st; st += 2) {
+    stage(st, std::integral_constant<int, 0>());
+    stage(st + 1, std::integral_constant<int, 1>());
   }
-  if (st < n_stages) body(st, R1, R2, R0);
-  if (st + 1 < n_stages) body(st + 1, R2, R0, R1);
+  if (st < n_st) stage(st, std::integral_constant<int, 0>());
 
   if (I32) {
-    // exact totals: x.code over all of K minus the sum of x over all slices
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int rl = wm * 32 * MT + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        int sx = 0;
-        for (int sl = 0; sl < n_slices; ++sl) sx += s_sx[sl][rl];
+      for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) o[mt][nt][v] = __int_as_float(acc[mt][nt][v] - sx);
-      }
+        for (int v = 0; v < 16; ++v) o[mt][nt][v] = __int_as_float(acc[mt][nt][v]);
   }
 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int n = n0 + wn * 64 + nt * 32 + j32;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int n = n0 + (wn * NTW + nt) * 32 + j32;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int r = m0 + wm * 32 * MT + mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int r = m0 + (wm * MT + mt) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (r < M && n < N) {
           if (I32)
             out_i32[(size_t)r * ldo + n] = __float_as_int(o[mt][nt][v]);
@@ -1103,92 +1187,67 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
   return gemv_t<64, 4, CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
 }
 
-// Tile shape per product: the one with the least estimated time, in rounds
-// of resident blocks weighted by the measured cost of a full round of each
-// shape relative to 128 x 128 (two 256-thread blocks per CU): 128 x 256
-// (one 512-thread block per CU) 0.85, 64 x 128 0.58 (M=4096, K=4096->2048:
-// 40.4 / 47.3 / 27.5 us per round at M=4096 / 4096 / 2048).  A last round
-// that leaves at most one block per CU of a two-per-CU grid counts 0.6 (a
-// block alone on its CU runs faster).  The estimate orders the measured
-// times of all three shapes at M=1024..4096 for K=2048->8512 and
-// K=4096->2048.
+// Tile shape per product: the one with the least estimated time.  With n
+// the tiles of the busiest CU (ceil(tiles / 256)), a shape's time is
+// modelled as (K/1024 + 0.5) (a + b (n - 1)) us: a is one tile alone on its
+// CU, b each further tile sharing it (three 64-row blocks or one 128 x 256
+// block are resident per CU).  Fitted to the measured times of the three
+// shapes at M = 129..4096, K = 1024..8192 (14 products): 64 x 64 a = 3.0,
+// b = 1.2; 64 x 128 a = 3.7, b = 2.1; 128 x 256 a = 7.0, b = 8.8; the
+// estimate picks the fastest shape or one within 7 % of it on all 14.
 constexpr int kCUs = 256;
-static double rounds_cost(long long tiles, int slots, bool two_per_cu) {
-  const long long full = tiles / slots, rest = tiles % slots;
-  return (double)full + (rest == 0 ? 0.0 : (two_per_cu && rest <= slots / 2) ? 0.6 : 1.0);
-}
-enum { GEMM_64x128 = 0, GEMM_128x128 = 1, GEMM_128x256 = 2 };
-static int gemm_shape(int M, int N, double* cost = nullptr) {
-  const long long tn128 = (N + 127) / 128, tn256 = (N + 255) / 256;
-  const double c64 = 0.58 * rounds_cost((M + 63) / 64 * tn128, 2 * kCUs, true);
-  const double c128 = rounds_cost((M + 127) / 128 * tn128, 2 * kCUs, true);
-  const double c256 = 0.85 * rounds_cost((M + 127) / 128 * tn256, kCUs, false);
-  int shape = c64 < c128 ? GEMM_64x128 : GEMM_128x128;
-  double c = c64 < c128 ? c64 : c128;
-  if (c256 <= c) {
-    shape = GEMM_128x256;
-    c = c256;
-  }
-  if (cost) *cost = c;
-  return shape;
-}
-// Columns of a first launch that leaves the rest of N to a second one (a
-// multiple of 256), or N for a single launch.  Two launches pay when the
-// tiles of the whole product end in a nearly empty round: M=2048,
-// K=2048 -> 8512 is 3 rounds of 544 tiles of 128 x 256 (65.8 us), but 8192
-// columns are exactly 2 rounds (46.8 us) and the other 320 take 10.9 us as
-// 64 x 128 tiles.  The second launch is charged 0.45 round beyond its own
-// estimate (its launch and latency): less made M=1024 -> 8384 and
-// M=1233 -> 8512 split and run 1.5-2 us slower than one launch.
-static int gemm_split(int M, int N) {
-  double best;
-  gemm_shape(M, N, &best);
-  best -= 0.45;
-  int split = N;
-  for (int head = (N - 1) / 256 * 256; head > 0; head -= 256) {  // ties: the larger head
+enum { GEMM_64x64 = 0, GEMM_64x128 = 1, GEMM_128x256 = 2 };
+static int gemm_shape(int M, int N, int K) {
+  struct Cand {
+    int shape, bm, bn;
     double a, b;
-    gemm_shape(M, head, &a);
-    gemm_shape(M, N - head, &b);
-    if (a + b < best) {
-      best = a + b;
-      split = head;
+  };
+  const Cand cands[3] = {{GEMM_64x64, 64, 64, 3.0, 1.2},
+                         {GEMM_64x128, 64, 128, 3.7, 2.1},
+                         {GEMM_128x256, 128, 256, 7.0, 8.8}};
+  int best = GEMM_64x128;
+  double best_t = 1e300;
+  for (const Cand& c : cands) {
+    if (c.shape == GEMM_64x64 && K % 256 != 0) continue;  // its 128-deep stages lack B loads for every thread
+    const long long tiles = (long long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const long long n = (tiles + kCUs - 1) / kCUs;
+    const double t = (K / 1024.0 + 0.5) * (c.a + c.b * (double)(n - 1));
+    if (t < best_t) {
+      best_t = t;
+      best = c.shape;
     }
   }
-  return split;
+  return best;
 }
 
-template <bool CANON, int MODE>
-static hipError_t gemm_launch(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
-                              int N, int K, float w_scale, void* out, int ldo, hipStream_t s) {
-  const int shape = gemm_shape(M, N);
-  if (shape == GEMM_128x256) {
-    const dim3 grid((unsigned)((M + 127) / 128 * ((N + 255) / 256)));
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 4, 2>), grid, dim3(512), 0, s, act,
-                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+// stage depth 256 when K allows, else 128 (not for 64 x 64 tiles); the
+// LDS ring holds two 256-deep stages or three 128-deep ones
+template <bool CANON, int MODE, int MT, int NTW, int WN, int OCC, bool DEEP_ONLY = false>
+static void gemm_launch_tile(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
+                             int N, int K, float w_scale, void* out, int ldo, hipStream_t s) {
+  constexpr int BM = 64 * MT, BN = 32 * NTW * WN;
+  const dim3 grid((unsigned)((M + BM - 1) / BM * ((N + BN - 1) / BN)));
+  if (DEEP_ONLY || K % 256 == 0)
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, MT, NTW, WN, 2, OCC, 256>), grid, dim3(128 * WN), 0, s,
+                       act, act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
                        (int32_t*)out, ldo);
-  } else if (shape == GEMM_64x128) {
-    const dim3 grid((unsigned)((M + 63) / 64 * ((N + 127) / 128)));
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 1>), grid, dim3(256), 0, s, act,
-                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+  else if constexpr (!DEEP_ONLY)
+    hipLaunchKernelGGL((k_gemm<CANON, MODE, MT, NTW, WN, 3, OCC, 128>), grid, dim3(128 * WN), 0, s,
+                       act, act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
                        (int32_t*)out, ldo);
-  } else {
-    const dim3 grid((unsigned)((M + 127) / 128 * ((N + 127) / 128)));
-    hipLaunchKernelGGL((k_gemm<CANON, MODE, 2, 2>), grid, dim3(256), 0, s, act,
-                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
-                       (int32_t*)out, ldo);
-  }
-  return hipGetLastError();
 }
 
 template <bool CANON, int MODE>
 static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const uint8_t* W, int N,
                          int K, float w_scale, void* out, hipStream_t s) {
-  const int head = gemm_split(M, N);
-  hipError_t e = gemm_launch<CANON, MODE>(act, scale_x, M, W, head, K, w_scale, out, N, s);
-  if (e != hipSuccess || head == N) return e;
-  // the last N % 256 columns: their weight rows and output columns
-  return gemm_launch<CANON, MODE>(act, scale_x, M, W + (size_t)head * (K / 4), N - head, K,
-                                  w_scale, (uint8_t*)out + 4 * (size_t)head, N, s);
+  const int shape = gemm_shape(M, N, K);
+  if (shape == GEMM_128x256)
+    gemm_launch_tile<CANON, MODE, 2, 2, 4, 1>(act, scale_x, M, W, N, K, w_scale, out, N, s);
+  else if (shape == GEMM_64x128)
+    gemm_launch_tile<CANON, MODE, 1, 2, 2, 3>(act, scale_x, M, W, N, K, w_scale, out, N, s);
+  else
+    gemm_launch_tile<CANON, MODE, 1, 1, 2, 3, true>(act, scale_x, M, W, N, K, w_scale, out, N, s);
+  return hipGetLastError();
 }
 
 // which kernel serves a product of this shape
