@@ -170,11 +170,16 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
 #pragma unroll
   for (int i = 0; i < G; ++i)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int c4 = 4 * (lane + 64 * i) + k;
-      xv[i][k] = ((const float4*)xr)[c4];
-      gv[i][k] = ((const float4*)gamma)[c4];
-    }
+    for (int k = 0; k < 4; ++k) xv[i][k] = ((const float4*)xr)[4 * (lane + 64 * i) + k];
+  // gamma is read after the sum of squares (the same rows for every token,
+  // so they come from L2): during the chains its registers stay free, which
+  // lets two waves share a SIMD at n = 4096 and four at n = 2048
+  auto load_gamma = [&]() {
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) gv[i][k] = ((const float4*)gamma)[4 * (lane + 64 * i) + k];
+  };
   float sum;
   if (fast) {
     // the pairwise tree: leaf group lane + 64 i, then the G wave sums
@@ -211,6 +216,7 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
     const float s2 = lane_f32(cs, 47), s3 = lane_f32(cs, 63);
     sum = __fadd_rn(__fadd_rn(__fadd_rn(s0, s1), s2), s3);
   }
+  load_gamma();
   // sum / K with K a power of two: an exact scaling, rounded like the division
   const float rms = cr_divf(1.0f, cr_sqrtf(__fadd_rn(__fmul_rn(sum, 1.0f / K), 1e-6f)));
 
