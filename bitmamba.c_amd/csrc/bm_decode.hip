@@ -347,9 +347,6 @@ __device__ float split_prologue(SplitIn<G, PRENORM>& in, const Lds& l, bool fast
   float4 (&xv)[G] = in.xv;
   const float4 (&gv)[G] = in.gv;
   const float4 (&gp)[PRENORM ? G : 1] = in.gp;
-  // slice sums are accumulated from R waves each: cleared before the first
-  // barrier below
-  if (R > 1 && tid < G) l.slices[tid] = 0;
   float rms;
   if (fast) {
     if (threadIdx.x >= 64) idle();
@@ -385,15 +382,11 @@ __device__ float split_prologue(SplitIn<G, PRENORM>& in, const Lds& l, bool fast
   const float max_abs = fmaxf(fmaxf(l.bc[8], l.bc[9]), fmaxf(l.bc[10], l.bc[11]));
   const float scale_x = cr_divf(127.0f, __fadd_rn(max_abs, 1e-5f));
   int q[CPT];
-  int qsum = 0;
 #pragma unroll
   for (int k = 0; k < G; ++k) {
     const float vv[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      q[4 * k + j] = (int)(int8_t)q8_of(vv[j], scale_x);
-      qsum += q[4 * k + j];
-    }
+    for (int j = 0; j < 4; ++j) q[4 * k + j] = (int)(int8_t)q8_of(vv[j], scale_x);
   }
   // this thread's nibbles of its group's four split-nibble words: columns
   // 2n (even) and 2n+1 (odd) of the group are nibble n; the thread's
@@ -434,14 +427,8 @@ __device__ float split_prologue(SplitIn<G, PRENORM>& in, const Lds& l, bool fast
     else
       *(uint32_t*)(xq_out + CPT * tid) = b[0];
   }
-  // a 1024-column slice is R waves (wave w's columns are slice w / R)
-  const int ssum = wave_sum_i32(qsum);
-  if (lane == 0) {
-    if constexpr (R == 1)
-      l.slices[wave] = ssum;
-    else
-      atomicAdd(&l.slices[wave / R], ssum);
-  }
+  // no slice sums here: the GEMV lanes take their share of each slice's sum
+  // of x from the nibbles they read (lane_sums)
   __syncthreads();
   return scale_x;
 }
@@ -470,7 +457,7 @@ __device__ __forceinline__ int dot64(uint4 w, const uint32_t (&xa)[16]) {
 // reduce a lane partial over its 16-lane slice group, subtract the slice's
 // sum of x, fold the slices of the T-lane row team in order into fp32
 // (src/kernel.c:255-256, 407-425)
-template <int P, int T>
+template <int P, int T, bool READ_SL = true>
 __device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32_t (&xa)[P][16],
                                               int (&xsl)[P]) {
   const int chunks = K >> 6;
@@ -486,7 +473,30 @@ __device__ __forceinline__ void load_lane_act(const Lds& l, int K, int u, uint32
       xa[p][4 * g + 3] = v.w;
     }
     const int sl = (p * T + u) >> 4;
-    xsl[p] = sl < slices_of(K) ? l.slices[sl] : 0;
+    xsl[p] = READ_SL && sl < slices_of(K) ? l.slices[sl] : 0;
+  }
+}
+
+// The lane's share of its slice's sum of x: its 64 columns from the split
+// nibbles it holds (x = lo + 16 hi, lo unsigned, hi signed).  Subtracted
+// from the lane's partial x.code before the 16-lane reduction, it makes the
+// slice total x.code - sum(x) (w = code - 1) without a reduction of x in
+// the prologue; exact in int32 either way.
+template <int P>
+__device__ __forceinline__ void lane_sums(const uint32_t (&xa)[P][16], int (&xs)[P]) {
+  constexpr uint32_t ones = 0x11111111u;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    uint32_t al = 0;
+    int ah = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      al = __builtin_amdgcn_udot8(xa[p][4 * g + 0], ones, al, false);
+      al = __builtin_amdgcn_udot8(xa[p][4 * g + 1], ones, al, false);
+      ah = __builtin_amdgcn_sdot8((int)xa[p][4 * g + 2], (int)ones, ah, false);
+      ah = __builtin_amdgcn_sdot8((int)xa[p][4 * g + 3], (int)ones, ah, false);
+    }
+    xs[p] = ah * 16 + (int)al;
   }
 }
 
@@ -602,8 +612,14 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   if (defer_rows && wave == 0) load_rows();
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
-  int xsl[P];
-  load_lane_act<P, T>(l, K, u, xa, xsl);
+  int xsl[P], xsd[P];  // slice sums (after the reduction) or lane shares (before it)
+  load_lane_act<P, T, !WP>(l, K, u, xa, xsl);
+  if constexpr (WP) {
+    lane_sums<P>(xa, xsd);
+  } else {
+#pragma unroll
+    for (int p = 0; p < P; ++p) xsd[p] = 0;
+  }
 
   float best_v = PICK == 2 ? -1e30f : -1e9f;
   int best_i = 0x7fffffff;
@@ -633,7 +649,8 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       float o = 0.0f;
 #pragma unroll
       for (int p = 0; p < P; ++p)
-        o = row_finish<T>(dot64(wv[it][p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+        o = row_finish<T>(dot64(wv[it][p], xa[p]) - xsd[p], xsl[p], p, slices_of(K), inv, o,
+                           unit_base);
       emit(grp * RPW + sub, o, resid[it]);
     }
   }
@@ -645,7 +662,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       const int j = p * T + u;
       const uint4 w = (r < N && j < chunks) ? *(const uint4*)(W + (size_t)r * wstride + 16 * j)
                                             : make_uint4(0, 0, 0, 0);
-      o = row_finish<T>(dot64(w, xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+      o = row_finish<T>(dot64(w, xa[p]) - xsd[p], xsl[p], p, slices_of(K), inv, o, unit_base);
     }
     emit(r, o, MODE == 1 && u == 0 && r < N ? out[r] : 0.0f);
   }
@@ -797,8 +814,14 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
   }
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
-  int xsl[P];
-  load_lane_act<P, T>(l, K, u, xa, xsl);
+  int xsl[P], xsd[P];  // slice sums (after the reduction) or lane shares (before it)
+  load_lane_act<P, T, !WP>(l, K, u, xa, xsl);
+  if constexpr (WP) {
+    lane_sums<P>(xa, xsd);
+  } else {
+#pragma unroll
+    for (int p = 0; p < P; ++p) xsd[p] = 0;
+  }
 
 #pragma unroll
   for (int it = 0; it < NPF; ++it) {
@@ -807,7 +830,8 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
       float o = 0.0f;
 #pragma unroll
       for (int p = 0; p < P; ++p)
-        o = row_finish<T>(dot64(wv[it][p], xa[p]), xsl[p], p, slices_of(K), inv, o, unit_base);
+        o = row_finish<T>(dot64(wv[it][p], xa[p]) - xsd[p], xsl[p], p, slices_of(K), inv, o,
+                           unit_base);
       const int r = grp * RPW + sub;
       if (u == 0 && r < kRowsCB) s_proj[r] = o;
     }
