@@ -160,11 +160,16 @@ __device__ __forceinline__ float4 scale4(const float4& x, float rms, const float
                      __fmul_rn(__fmul_rn(x.z, rms), g.z), __fmul_rn(__fmul_rn(x.w, rms), g.w));
 }
 
-__device__ __forceinline__ uint32_t q8_of(float v, float scale_x) {
+// round half away from zero and clamp (src/kernel.c:115-125): t + 0.5 with
+// t's sign (copysign gives -0.5 only for t < 0 or t = -0, where t >= 0 ?
+// 0.5 : -0.5 would give +0.5 for -0; both then truncate to 0), one med3
+__device__ __forceinline__ int q8i_of(float v, float scale_x) {
   const float t = __fmul_rn(v, scale_x);
-  int iv = (int)__fadd_rn(t, t >= 0.0f ? 0.5f : -0.5f);
-  iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
-  return (uint32_t)(iv & 255);
+  const int iv = (int)__fadd_rn(t, __builtin_copysignf(0.5f, t));
+  return iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+}
+__device__ __forceinline__ uint32_t q8_of(float v, float scale_x) {
+  return (uint32_t)(q8i_of(v, scale_x) & 255);
 }
 
 // int8 quantization of (x*rms)*gamma (src/kernel.c:93-128, 358-386) into the
@@ -386,7 +391,7 @@ __device__ float split_prologue(SplitIn<G, PRENORM>& in, const Lds& l, bool fast
   for (int k = 0; k < G; ++k) {
     const float vv[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) q[4 * k + j] = (int)(int8_t)q8_of(vv[j], scale_x);
+    for (int j = 0; j < 4; ++j) q[4 * k + j] = q8i_of(vv[j], scale_x);
   }
   // this thread's nibbles of its group's four split-nibble words: columns
   // 2n (even) and 2n+1 (odd) of the group are nibble n; the thread's
