@@ -1069,6 +1069,23 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void k_gemm(const uint8_t* __res
         for (int v = 0; v < 16; ++v) o[mt][nt][v] = __int_as_float(acc[mt][nt][v]);
   }
 
+  if (MODE == 1 && !I32) {
+    // residual add: every residual load in flight before the first add (a
+    // guarded load + add + store per element waits out one load latency per
+    // element); rows and columns past M / N read the last one and store nothing
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int n = min(n0 + (wn * NTW + nt) * 32 + j32, N - 1);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = min(m0 + (wm * MT + mt) * 32 + 8 * (v >> 2) + 4 * h + (v & 3), M - 1);
+          o[mt][nt][v] = __fadd_rn(out[(size_t)r * ldo + n], o[mt][nt][v]);
+        }
+      }
+  }
+
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1081,8 +1098,7 @@ __global__ __launch_bounds__(64 * WM * WN, OCC) void k_gemm(const uint8_t* __res
           if (I32)
             out_i32[(size_t)r * ldo + n] = __float_as_int(o[mt][nt][v]);
           else
-            out[(size_t)r * ldo + n] =
-                MODE == 1 ? __fadd_rn(out[(size_t)r * ldo + n], o[mt][nt][v]) : o[mt][nt][v];
+            out[(size_t)r * ldo + n] = o[mt][nt][v];
         }
       }
     }
