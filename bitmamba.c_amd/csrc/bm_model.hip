@@ -111,6 +111,26 @@ __global__ __launch_bounds__(256) void k_ssm_prep(const float* __restrict__ proj
   // the heads this block's channels belong to: h_first .. h_first + nhb - 1
   const int h_first = (blockIdx.x * blockDim.x) / hd;
   const int nhb = min(di - 1, (int)(blockIdx.x * blockDim.x + blockDim.x) - 1) / hd - h_first + 1;
+  // the channel's inputs first, so that their loads are in flight while the
+  // head threads run the softplus / exp chains below
+  const bool live = idx < di;
+  const int ci = live ? idx : di - 1;
+  const int h = ci / hd, c = ci - h * hd;
+  const size_t xoff = (size_t)h * (2 * hd + 3) + hd + c;
+  const int pos0 = ctl[CTL_POS];
+  // inputs of tokens tq-3 .. tq+3 of the chunk: from the batch, or from the
+  // conv ring for the three tokens before the prompt (x_{-j} sits at ring
+  // position pos0 + 3 - j); past the chunk's end: unused
+  float xv[7];
+#pragma unroll
+  for (int k = 0; k < 7; ++k) {
+    const int tp = tq - 3 + k, tg = t0 + tp;
+    xv[k] = tp >= nt ? 0.0f
+            : tg >= 0 ? proj[(size_t)tg * pd + xoff]
+                      : cs[(size_t)((pos0 + 3 + tg) % 3) * di + ci];
+  }
+  const float w0 = cw[ci], w1 = cw[di + ci], w2 = cw[2 * di + ci], w3 = cw[3 * di + ci];
+  const float bias = cb[ci], Dv = D[ci];
   for (int w = threadIdx.x; w < 4 * nhb; w += blockDim.x) {
     const int e = w / nhb, hb = w - e * nhb, t = tq + e, h = h_first + hb;
     float decay = 1.0f;
@@ -124,23 +144,7 @@ __global__ __launch_bounds__(256) void k_ssm_prep(const float* __restrict__ proj
     pre[PL.decay + (size_t)h * PL.nqa * 4 + t] = decay;
   }
   __syncthreads();
-  if (idx >= di) return;
-  const int h = idx / hd, c = idx - h * hd;
-  const size_t xoff = (size_t)h * (2 * hd + 3) + hd + c;
-  const int pos0 = ctl[CTL_POS];
-  // inputs of tokens tq-3 .. tq+3 of the chunk: from the batch, or from the
-  // conv ring for the three tokens before the prompt (x_{-j} sits at ring
-  // position pos0 + 3 - j); past the chunk's end: unused
-  float xv[7];
-#pragma unroll
-  for (int k = 0; k < 7; ++k) {
-    const int tp = tq - 3 + k, tg = t0 + tp;
-    xv[k] = tp >= nt ? 0.0f
-            : tg >= 0 ? proj[(size_t)tg * pd + xoff]
-                      : cs[(size_t)((pos0 + 3 + tg) % 3) * di + idx];
-  }
-  const float w0 = cw[idx], w1 = cw[di + idx], w2 = cw[2 * di + idx], w3 = cw[3 * di + idx];
-  const float bias = cb[idx], Dv = D[idx];
+  if (!live) return;
   float xb[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
