@@ -1217,8 +1217,12 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
 // shapes at M = 129..4096, K = 1024..8192 (14 products): 64 x 64 a = 3.0,
 // b = 1.2; 64 x 128 a = 3.7, b = 2.1; 128 x 256 a = 7.0, b = 8.8; the
 // estimate picks the fastest shape or one within 7 % of it on all 14.
+// Where 64 x 128 tiles leave CUs idle (at most one tile per CU) and K is a
+// multiple of 256, 32 x 128 tiles (4 waves of 32 x 32) double the blocks:
+// M = 1024, K = 4096 -> 2048 in 14.0 us against 15.6; with more tiles they
+// lose (M = 1024, K = 2048 -> 8384: 27.5 against 26.4 us).
 constexpr int kCUs = 256;
-enum { GEMM_64x64 = 0, GEMM_64x128 = 1, GEMM_128x256 = 2 };
+enum { GEMM_64x64 = 0, GEMM_64x128 = 1, GEMM_128x256 = 2, GEMM_32x128 = 3 };
 static int gemm_shape(int M, int N, int K) {
   struct Cand {
     int shape, bm, bn;
@@ -1239,6 +1243,8 @@ static int gemm_shape(int M, int N, int K) {
       best = c.shape;
     }
   }
+  const long long tiles64x128 = (long long)((M + 63) / 64) * ((N + 127) / 128);
+  if (best == GEMM_64x128 && tiles64x128 <= kCUs && K % 256 == 0) best = GEMM_32x128;
   return best;
 }
 
@@ -1265,11 +1271,15 @@ static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const 
   const int shape = gemm_shape(M, N, K);
   // 128 x 256: 2 x 4 waves of 64 x 64; 64 x 128: 1 x 4 waves of 64 x 32 (half
   // the B decode per MFMA of 2 x 2 waves of 32 x 64, 2-5 % faster);
-  // 64 x 64: 2 x 2 waves of 32 x 32
+  // 64 x 64: 2 x 2 waves of 32 x 32; 32 x 128: 1 x 4 waves of 32 x 32 (four
+  // blocks per CU)
   if (shape == GEMM_128x256)
     gemm_launch_tile<CANON, MODE, 2, 2, 2, 4, 1>(act, scale_x, M, W, N, K, w_scale, out, N, s);
   else if (shape == GEMM_64x128)
     gemm_launch_tile<CANON, MODE, 2, 1, 1, 4, 3>(act, scale_x, M, W, N, K, w_scale, out, N, s);
+  else if (shape == GEMM_32x128)
+    gemm_launch_tile<CANON, MODE, 1, 1, 1, 4, 4, true>(act, scale_x, M, W, N, K, w_scale, out, N,
+                                                       s);
   else
     gemm_launch_tile<CANON, MODE, 1, 1, 2, 2, 3, true>(act, scale_x, M, W, N, K, w_scale, out, N,
                                                        s);

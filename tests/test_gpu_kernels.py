@@ -187,7 +187,10 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (1233, 256, 8512), (2100, 128, 2048), (1920, 256, 8512),
                                    # GEMM stage counts: 3 and 5 stages of 128 (the ring's
                                    # prologue and tail waits), 64 stages of 256
-                                   (320, 384, 300), (513, 640, 1000), (600, 16384, 130)])
+                                   (320, 384, 300), (513, 640, 1000), (600, 16384, 130),
+                                   # 32x128 tiles (64x128 would leave CUs idle), ragged
+                                   # last row and column tiles
+                                   (520, 256, 3000)])
 def test_gemm_i32_exact(hip, M, K, N):
     note("gemm i32 M=%d K=%d N=%d" % (M, K, N))
     r = rnd(M * 3 + K + N)
@@ -291,7 +294,9 @@ FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257)
              (64, 2048, 8384), (100, 4096, 2048), (256, 4096, 2048), (77, 3072, 96),
              (128, 2048, 8384),
              # the MFMA GEMM with partial last slices (K = 1.5, 3 and 5 slices of 1024)
-             (300, 1536, 520), (400, 3072, 200), (260, 5120, 130)]
+             (300, 1536, 520), (400, 3072, 200), (260, 5120, 130),
+             # 32x128 tiles (at most one 64x128 tile per CU), ragged last tiles
+             (700, 1024, 2000)]
 
 
 @pytest.mark.parametrize("M,K,N", FP_SHAPES)
