@@ -190,7 +190,9 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (320, 384, 300), (513, 640, 1000), (600, 16384, 130),
                                    # 32x128 tiles (64x128 would leave CUs idle), ragged
                                    # last row and column tiles
-                                   (520, 256, 3000)])
+                                   (520, 256, 3000),
+                                   # 64x256 tiles (two 64x128 tiles per CU), ragged
+                                   (1100, 256, 3000)])
 def test_gemm_i32_exact(hip, M, K, N):
     note("gemm i32 M=%d K=%d N=%d" % (M, K, N))
     r = rnd(M * 3 + K + N)
@@ -296,7 +298,9 @@ FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257)
              # the MFMA GEMM with partial last slices (K = 1.5, 3 and 5 slices of 1024)
              (300, 1536, 520), (400, 3072, 200), (260, 5120, 130),
              # 32x128 tiles (at most one 64x128 tile per CU), ragged last tiles
-             (700, 1024, 2000)]
+             (700, 1024, 2000),
+             # 64x256 tiles (two 64x128 tiles per CU), ragged last tiles
+             (1000, 2048, 3100)]
 
 
 @pytest.mark.parametrize("M,K,N", FP_SHAPES)

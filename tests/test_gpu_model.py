@@ -253,10 +253,10 @@ def test_odd_shapes_vs_oracle(hip, vocab, d_model, n_heads, penalty, sampler):
 # 128x256 (three SSM chunks); 255M width, 1030 tokens: in_proj 128x256,
 # out_proj 64x128, two SSM chunks; d_model 320: out_proj (K=640 -> N=320)
 # in 64x128 tiles with 128-deep stages, its residual add over ragged last
-# row and column tiles
+# row and column tiles; 1600 tokens: out_proj in 64x256 tiles
 @pytest.mark.parametrize("d_model,n_heads,n_tokens", [(1024, 32, 1030), (2048, 64, 300),
                                                       (2048, 64, 1220), (2048, 64, 2100),
-                                                      (320, 10, 300)])
+                                                      (320, 10, 300), (2048, 64, 1600)])
 def test_wide_model_long_prefill_vs_oracle(hip, d_model, n_heads, n_tokens):
     """Long prompts at the 255M and 1B widths (two layers, 2000-token
     vocabulary): the batched path with MFMA GEMM tiles, the quantize kernels
