@@ -54,7 +54,7 @@ hipError_t launch_quantize(const float *x, int M, int n, int x_stride,
                            const float *gamma, float *x_norm, int8_t *xq,
                            int quant_stride, float *scale_x, uint8_t *act,
                            hipStream_t s, bool nibbles = true, bool fast = false);
-hipError_t launch_prep_i8(const int8_t *xq, int M, int ldx, int K, uint8_t *act,
+hipError_t launch_prep_i8(const int8_t *xq, int M, int ldx, int K, uint8_t *act, bool nib,
                           hipStream_t s);
 // Output modes of the products: fp32 store, fp32 accumulate (out += o, the
 // residual add of src/model.c:1214-1215, 1139-1142), exact int32 totals.

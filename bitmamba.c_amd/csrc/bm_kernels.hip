@@ -275,24 +275,36 @@ __global__ __launch_bounds__(G == 4 ? 128 : 256) void k_quantize_wave(const floa
   }
 }
 
-// int8 activations given directly (stress shape): workspace only
+// int8 activations given directly (stress shape): workspace only.  A row
+// that starts on 16 bytes is read 16 bytes per thread; NIB: also the split
+// nibbles, which only the per-token GEMV kernels read
+template <bool NIB>
 __global__ __launch_bounds__(QT) void k_prep_i8(const int8_t* __restrict__ xq, int ldx, int K,
                                                 uint8_t* __restrict__ act, size_t act_stride) {
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int8_t* __restrict__ xr = xq + (size_t)m * ldx;
   uint8_t* __restrict__ arow = act + (size_t)m * act_stride;
   const int n_groups = (K + 15) >> 4;
+  const bool vec = ((uintptr_t)xr & 15) == 0;
   for (int g0 = 0; g0 < n_groups; g0 += QT) {
     const int g = g0 + tid;
     int q[16];
     int qsum = 0;
+    if (vec && 16 * g + 15 < K) {
+      const int4 v = *(const int4*)(xr + 16 * g);
+      const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int c = 16 * g + j;
-      q[j] = c < K ? (int)xr[c] : 0;
-      qsum += q[j];
+      for (int j = 0; j < 16; ++j) q[j] = (int)(int8_t)(w[j >> 2] >> (8 * (j & 3)));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int c = 16 * g + j;
+        q[j] = c < K ? (int)xr[c] : 0;
+      }
     }
-    if (g < n_groups) write_act_group(arow, K, g, q);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) qsum += q[j];
+    if (g < n_groups) write_act_group(arow, K, g, q, NIB);
     const int s = wave_sum_i32(g < n_groups ? qsum : 0);
     const int slice = (g0 >> 6) + wave;
     if (lane == 0 && slice < slices_of(K)) ((int*)arow)[slice] = s;
@@ -1152,9 +1164,15 @@ hipError_t launch_rms_norm(const float* x, int n, const float* gamma, float* out
   return hipGetLastError();
 }
 
-hipError_t launch_prep_i8(const int8_t* xq, int M, int ldx, int K, uint8_t* act, hipStream_t s) {
+hipError_t launch_prep_i8(const int8_t* xq, int M, int ldx, int K, uint8_t* act, bool nib,
+                          hipStream_t s) {
   if (M <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_prep_i8, dim3(M), dim3(QT), 0, s, xq, ldx, K, act, act_row_bytes(K));
+  if (nib)
+    hipLaunchKernelGGL(k_prep_i8<true>, dim3(M), dim3(QT), 0, s, xq, ldx, K, act,
+                       act_row_bytes(K));
+  else
+    hipLaunchKernelGGL(k_prep_i8<false>, dim3(M), dim3(QT), 0, s, xq, ldx, K, act,
+                       act_row_bytes(K));
   return hipGetLastError();
 }
 

@@ -660,7 +660,9 @@ extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
     bm_set_error("ternary_gemm_i32: act workspace required");
     return -2;
   }
-  BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act, s), -1);
+  BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act,
+                                      bm::product_reads_nibbles(M, N, K), s),
+                   -1);
   BM_HIP_CHECK_RET(bm::launch_product((const uint8_t*)act, nullptr, M, packed, N, K, 0.0f,
                                       canonical != 0, out, bm::MODE_I32, s),
                    -1);
@@ -769,7 +771,9 @@ extern "C" int bm_hip_ternary_gemm_i32_tiled_dev(const int8_t* xq, int M, int ld
     return -2;
   }
   hipStream_t s = stream_or_default(stream);
-  BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act, s), -1);
+  BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act,
+                                      bm::product_reads_nibbles(M, N, K), s),
+                   -1);
   BM_HIP_CHECK_RET(bm::launch_gemm_tiled((const uint8_t*)act, nullptr, M, tiled, N, K, 0.0f, out,
                                          bm::MODE_I32, s),
                    -1);
