@@ -1230,34 +1230,35 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
 // Tile shape per product: the one with the least estimated time.  With n
 // the tiles of the busiest CU (ceil(tiles / 256)), a shape's time is
 // modelled as (K/1024 + 0.5) (a + b (n - 1)) us: a is one tile alone on its
-// CU, b each further tile sharing it (three 64-row blocks or one 128 x 256
-// block are resident per CU).  Fitted to the measured times of the three
+// CU, b each further tile sharing it.  Fitted to the measured times of three
 // shapes at M = 129..4096, K = 1024..8192 (14 products): 64 x 64 a = 3.0,
 // b = 1.2; 64 x 128 a = 3.7, b = 2.1; 128 x 256 a = 7.0, b = 8.8; the
 // estimate picks the fastest shape or one within 7 % of it on all 14.
-// Where 64 x 128 tiles leave CUs idle (at most one tile per CU) and K is a
-// multiple of 256, 32 x 128 tiles (4 waves of 32 x 32) double the blocks:
-// M = 1024, K = 4096 -> 2048 in 14.0 us against 15.6; with more tiles they
-// lose (M = 1024, K = 2048 -> 8384: 27.5 against 26.4 us).  Where they
+// Tiles of 4096 outputs run as 32 x 128 (4 waves of 32 x 32, four blocks
+// per CU), which measured 2-11 % faster than 64 x 64 on the seven products
+// the estimate gives them (M = 300..1536, K = 1024..4096), and also replace
+// 64 x 128 tiles that would leave CUs idle (at most one per CU): M = 1024,
+// K = 4096 -> 2048 in 14.0 us against 15.6; with more tiles they lose
+// (M = 1024, K = 2048 -> 8384: 27.5 against 26.4 us).  Where 64 x 128 tiles
 // come two per CU, 64 x 256 tiles (8 waves of 64 x 32, one block per CU)
 // read each activation tile once instead of twice and measured 3-8 %
 // faster on seven such products (M = 2048, K = 4096 -> 2048: 22.1 against
 // 23.1 us); at more tiles per CU they lose (M = 2048, K = 2048 -> 8512:
-// 53.6 against 45.3 us).
+// 53.6 against 45.3 us).  32 x 128 and 64 x 256 tiles take K % 256 == 0.
 constexpr int kCUs = 256;
-enum { GEMM_64x64 = 0, GEMM_64x128 = 1, GEMM_128x256 = 2, GEMM_32x128 = 3, GEMM_64x256 = 4 };
+enum { GEMM_32x128 = 0, GEMM_64x128 = 1, GEMM_128x256 = 2, GEMM_64x256 = 3 };
 static int gemm_shape(int M, int N, int K) {
   struct Cand {
     int shape, bm, bn;
     double a, b;
   };
-  const Cand cands[3] = {{GEMM_64x64, 64, 64, 3.0, 1.2},
+  const Cand cands[3] = {{GEMM_32x128, 64, 64, 3.0, 1.2},  // fitted on 64 x 64 tiles
                          {GEMM_64x128, 64, 128, 3.7, 2.1},
                          {GEMM_128x256, 128, 256, 7.0, 8.8}};
   int best = GEMM_64x128;
   double best_t = 1e300;
   for (const Cand& c : cands) {
-    if (c.shape == GEMM_64x64 && K % 256 != 0) continue;  // its 128-deep stages lack B loads for every thread
+    if (c.shape == GEMM_32x128 && K % 256 != 0) continue;
     const long long tiles = (long long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const long long n = (tiles + kCUs - 1) / kCUs;
     const double t = (K / 1024.0 + 0.5) * (c.a + c.b * (double)(n - 1));
@@ -1267,16 +1268,12 @@ static int gemm_shape(int M, int N, int K) {
     }
   }
   const long long tiles64x128 = (long long)((M + 63) / 64) * ((N + 127) / 128);
-  if (best == GEMM_64x128 && K % 256 == 0) {
-    if (tiles64x128 <= kCUs)
-      best = GEMM_32x128;
-    else if (tiles64x128 <= 2 * kCUs)
-      best = GEMM_64x256;
-  }
+  if (best == GEMM_64x128 && K % 256 == 0 && tiles64x128 <= 2 * kCUs)
+    best = tiles64x128 <= kCUs ? GEMM_32x128 : GEMM_64x256;
   return best;
 }
 
-// stage depth 256 when K allows, else 128 (not for 64 x 64 tiles); the
+// stage depth 256 when K allows, else 128 (DEEP_ONLY shapes: 256 only); the
 // LDS ring holds two 256-deep stages or three 128-deep ones
 template <bool CANON, int MODE, int MT, int NTW, int WM, int WN, int OCC, bool DEEP_ONLY = false>
 static void gemm_launch_tile(const uint8_t* act, const float* scale_x, int M, const uint8_t* W,
@@ -1299,20 +1296,16 @@ static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const 
   const int shape = gemm_shape(M, N, K);
   // 128 x 256: 2 x 4 waves of 64 x 64; 64 x 128: 1 x 4 waves of 64 x 32 (half
   // the B decode per MFMA of 2 x 2 waves of 32 x 64, 2-5 % faster);
-  // 64 x 64: 2 x 2 waves of 32 x 32; 32 x 128: 1 x 4 waves of 32 x 32 (four
-  // blocks per CU); 64 x 256: 1 x 8 waves of 64 x 32
+  // 64 x 256: 1 x 8 waves of 64 x 32; 32 x 128: 1 x 4 waves of 32 x 32
   if (shape == GEMM_128x256)
     gemm_launch_tile<CANON, MODE, 2, 2, 2, 4, 1>(act, scale_x, M, W, N, K, w_scale, out, N, s);
   else if (shape == GEMM_64x128)
     gemm_launch_tile<CANON, MODE, 2, 1, 1, 4, 3>(act, scale_x, M, W, N, K, w_scale, out, N, s);
-  else if (shape == GEMM_32x128)
-    gemm_launch_tile<CANON, MODE, 1, 1, 1, 4, 4, true>(act, scale_x, M, W, N, K, w_scale, out, N,
-                                                       s);
   else if (shape == GEMM_64x256)
     gemm_launch_tile<CANON, MODE, 2, 1, 1, 8, 2, true>(act, scale_x, M, W, N, K, w_scale, out, N,
                                                        s);
   else
-    gemm_launch_tile<CANON, MODE, 1, 1, 2, 2, 3, true>(act, scale_x, M, W, N, K, w_scale, out, N,
+    gemm_launch_tile<CANON, MODE, 1, 1, 1, 4, 4, true>(act, scale_x, M, W, N, K, w_scale, out, N,
                                                        s);
   return hipGetLastError();
 }

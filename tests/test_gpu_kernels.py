@@ -180,7 +180,7 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (1100, 1024, 700), (48, 16384, 96), (2, 2048, 77),
                                    (31, 4096, 300), (5, 8192, 33), (97, 4096, 200),
                                    (256, 2048, 64),
-                                   # GEMM tiles 64x64 (700x2048x1100, 1100x1024x700), 64x128
+                                   # GEMM tiles 32x128 (700x2048x1100, 1100x1024x700), 64x128
                                    # (300x1152x260 in 128-deep stages, 1233x256x8512 in
                                    # 256-deep ones), 128x256 (2100x128x2048: 128-deep,
                                    # 1920x256x8512: 256-deep)
