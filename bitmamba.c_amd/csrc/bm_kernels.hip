@@ -1244,7 +1244,11 @@ static hipError_t gemv_dispatch(const uint8_t* act, const float* scale_x, int M,
 // read each activation tile once instead of twice and measured 3-8 %
 // faster on seven such products (M = 2048, K = 4096 -> 2048: 22.1 against
 // 23.1 us); at more tiles per CU they lose (M = 2048, K = 2048 -> 8512:
-// 53.6 against 45.3 us).  32 x 128 and 64 x 256 tiles take K % 256 == 0.
+// 53.6 against 45.3 us).  128 x 256 tiles win only at long K or many tiles
+// per CU (K >= 8192: 3-15 % faster than 64 x 128 on six products; M = 4096,
+// K = 4096 -> 8192, four tiles per CU: 5 %) and lost 3-19 % on the four
+// shorter products the estimate gave them (M = 1600..2560, K = 2048, 4096),
+// so they are considered only there.  All but 64 x 128 take K % 256 == 0.
 constexpr int kCUs = 256;
 enum { GEMM_32x128 = 0, GEMM_64x128 = 1, GEMM_128x256 = 2, GEMM_64x256 = 3 };
 static int gemm_shape(int M, int N, int K) {
@@ -1258,9 +1262,10 @@ static int gemm_shape(int M, int N, int K) {
   int best = GEMM_64x128;
   double best_t = 1e300;
   for (const Cand& c : cands) {
-    if (c.shape == GEMM_32x128 && K % 256 != 0) continue;
+    if (c.shape != GEMM_64x128 && K % 256 != 0) continue;
     const long long tiles = (long long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const long long n = (tiles + kCUs - 1) / kCUs;
+    if (c.shape == GEMM_128x256 && K < 8192 && n < 4) continue;
     const double t = (K / 1024.0 + 0.5) * (c.a + c.b * (double)(n - 1));
     if (t < best_t) {
       best_t = t;
@@ -1298,7 +1303,8 @@ static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const 
   // the B decode per MFMA of 2 x 2 waves of 32 x 64, 2-5 % faster);
   // 64 x 256: 1 x 8 waves of 64 x 32; 32 x 128: 1 x 4 waves of 32 x 32
   if (shape == GEMM_128x256)
-    gemm_launch_tile<CANON, MODE, 2, 2, 2, 4, 1>(act, scale_x, M, W, N, K, w_scale, out, N, s);
+    gemm_launch_tile<CANON, MODE, 2, 2, 2, 4, 1, true>(act, scale_x, M, W, N, K, w_scale, out, N,
+                                                       s);
   else if (shape == GEMM_64x128)
     gemm_launch_tile<CANON, MODE, 2, 1, 1, 4, 3>(act, scale_x, M, W, N, K, w_scale, out, N, s);
   else if (shape == GEMM_64x256)

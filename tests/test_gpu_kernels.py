@@ -181,9 +181,10 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (31, 4096, 300), (5, 8192, 33), (97, 4096, 200),
                                    (256, 2048, 64),
                                    # GEMM tiles 32x128 (700x2048x1100, 1100x1024x700), 64x128
-                                   # (300x1152x260 in 128-deep stages, 1233x256x8512 in
-                                   # 256-deep ones), 128x256 (2100x128x2048: 128-deep,
-                                   # 1920x256x8512: 256-deep)
+                                   # (300x1152x260 and 2100x128x2048 in 128-deep stages,
+                                   # 1233x256x8512 and 1920x256x8512 in 256-deep ones);
+                                   # 128x256 tiles (K >= 8192 or four per CU) run in the
+                                   # M=4096 stress tests
                                    (1233, 256, 8512), (2100, 128, 2048), (1920, 256, 8512),
                                    # GEMM stage counts: 3 and 5 stages of 128 (the ring's
                                    # prologue and tail waits), 64 stages of 256
