@@ -184,7 +184,7 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    # (300x1152x260 and 2100x128x2048 in 128-deep stages,
                                    # 1233x256x8512 and 1920x256x8512 in 256-deep ones);
                                    # 128x256 tiles (K >= 8192 or four per CU) run in the
-                                   # M=4096 stress tests
+                                   # M=4096 stress tests and test_gemm_128x256_ragged
                                    (1233, 256, 8512), (2100, 128, 2048), (1920, 256, 8512),
                                    # GEMM stage counts: 3 and 5 stages of 128 (the ring's
                                    # prologue and tail waits), 64 stages of 256
@@ -237,6 +237,24 @@ def test_stress_m4096_sampled_and_linear(hip):
     ga = gpu_gemm_i32(hip, a, packed, N, K, 1)
     gb = gpu_gemm_i32(hip, b, packed, N, K, 1)
     np.testing.assert_array_equal(ga + gb, got[:256])
+
+
+def test_gemm_128x256_ragged(hip):
+    """128x256 tiles (K = 8192) with ragged last row and column tiles
+    (M = N = 2100): every total of the last row tile and of the last column
+    tile exact, plus sampled entries."""
+    M, K, N = 2100, 8192, 2100
+    note("gemm 128x256 ragged M=%d K=%d N=%d" % (M, K, N))
+    packed = bh.synth_ternary(11, 1, N, K, bh.SYNTH_P0_60)
+    xq = bh.synth_int8(11, 3, (M, K))
+    got = gpu_gemm_i32(hip, xq, packed, N, K, canonical=1)
+    w = native.decode_dense(packed, K).astype(np.int64)
+    np.testing.assert_array_equal(got[2048:], xq[2048:].astype(np.int64) @ w.T)
+    np.testing.assert_array_equal(got[:, 2048:], xq.astype(np.int64) @ w[2048:].T)
+    r = rnd(12)
+    ms = r.integers(0, M, 64)
+    ns = r.integers(0, N, 64)
+    np.testing.assert_array_equal(got[np.ix_(ms, ns)], xq[ms].astype(np.int64) @ w[ns].T)
 
 
 def test_stress_m4096_full_exact(hip):
