@@ -86,10 +86,6 @@ SIGNATURES = {
     "bm_hip_noalloc_scratch_bytes": (_sz, []),
     "bm_hip_i8_act_bytes": (_sz, [_i, _i]),
     "bm_hip_ternary_gemm_i32_dev": (_i, [_vp, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp]),
-    "bm_hip_tiled_bytes": (_sz, [_i, _i]),
-    "bm_hip_tile_weights_dev": (_i, [_vp, _i, _i, _i, _vp, _vp]),
-    "bm_hip_bitlinear_tiled_dev": (_i, [_vp, _vp, _i, _vp, _i, _i, _f, _vp, _vp]),
-    "bm_hip_ternary_gemm_i32_tiled_dev": (_i, [_vp, _i, _i, _vp, _i, _i, _vp, _vp, _vp]),
     "bm_hip_model_load": (_vp, [_vp, _sz]),
     "bm_hip_model_free": (None, [_vp]),
     "bm_hip_model_config": (_i, [_vp, _i]),

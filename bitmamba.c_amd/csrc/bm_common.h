@@ -86,17 +86,4 @@ hipError_t launch_dropin(const float *x, int K, const float *gamma, const uint8_
                          float w_scale, float *out, float *xn, int8_t *xq, unsigned *flags,
                          unsigned seq, hipStream_t s);
 
-// MFMA tile layout of packed weights (bm_gemm.hip): [ceil(N/32)][K/128]
-// blocks of 1 KB, each the 32 packed bytes of one 128-column stage of 32
-// consecutive rows, row after row; code 11 rewritten to 10.  K % 128 == 0.
-size_t tiled_bytes(int N, int K);
-hipError_t launch_tile_weights(const uint8_t *W, int N, int K, bool canonical, uint8_t *T,
-                               hipStream_t s);
-// GEMM on tiled weights (two K-groups per block); shapes it covers: any M
-// and N, K % 256 == 0, and for fp32 outputs K up to 4096 (int32 up to 16384)
-bool gemm_tiled_supported(int M, int K, int mode);
-hipError_t launch_gemm_tiled(const uint8_t *act, const float *scale_x, int M,
-                             const uint8_t *tiled, int N, int K, float w_scale, void *out,
-                             int mode, hipStream_t s);
-
 }  // namespace bm

@@ -724,62 +724,6 @@ extern "C" int bm_hip_bitlinear_noalloc_dev(const float* x, int M, int K, const 
 
 extern "C" size_t bm_hip_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
-extern "C" size_t bm_hip_tiled_bytes(int N, int K) {
-  if (N <= 0 || K <= 0 || K % 128 != 0) return 0;
-  return bm::tiled_bytes(N, K);
-}
-
-extern "C" int bm_hip_tile_weights_dev(const uint8_t* packed, int N, int K, int canonical,
-                                       uint8_t* tiled, void* stream) {
-  if (!bm_hip_init()) return -1;
-  if (N <= 0 || K <= 0 || K % 128 != 0 || !packed || !tiled ||
-      ((uintptr_t)packed & 15) || ((uintptr_t)tiled & 15)) {
-    bm_set_error("tile_weights: needs K %% 128 == 0 and 16-byte aligned buffers (N=%d K=%d)", N,
-                 K);
-    return -2;
-  }
-  BM_HIP_CHECK_RET(bm::launch_tile_weights(packed, N, K, canonical != 0, tiled,
-                                           stream_or_default(stream)),
-                   -1);
-  return 0;
-}
-
-extern "C" int bm_hip_bitlinear_tiled_dev(const void* act, const float* scale_x, int M,
-                                          const uint8_t* tiled, int N, int K, float w_scale,
-                                          float* out, void* stream) {
-  if (!bm_hip_init()) return -1;
-  if (M < 1 || N <= 0 || !act || !scale_x || !tiled || !out ||
-      !bm::gemm_tiled_supported(M, K, bm::MODE_STORE)) {
-    bm_set_error("bitlinear_tiled: invalid arguments or K=%d not covered (K %% 256 == 0, "
-                 "K <= 4096)", K);
-    return -2;
-  }
-  BM_HIP_CHECK_RET(bm::launch_gemm_tiled((const uint8_t*)act, scale_x, M, tiled, N, K, w_scale,
-                                         out, bm::MODE_STORE, stream_or_default(stream)),
-                   -1);
-  return 0;
-}
-
-extern "C" int bm_hip_ternary_gemm_i32_tiled_dev(const int8_t* xq, int M, int ldx,
-                                                 const uint8_t* tiled, int N, int K,
-                                                 int32_t* out, void* act, void* stream) {
-  if (!bm_hip_init()) return -1;
-  if (M < 1 || N <= 0 || ldx < K || !xq || !tiled || !out || !act ||
-      !bm::gemm_tiled_supported(M, K, bm::MODE_I32)) {
-    bm_set_error("ternary_gemm_i32_tiled: invalid arguments or K=%d not covered "
-                 "(K %% 256 == 0, K <= 16384)", K);
-    return -2;
-  }
-  hipStream_t s = stream_or_default(stream);
-  BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act,
-                                      bm::product_reads_nibbles(M, N, K), s),
-                   -1);
-  BM_HIP_CHECK_RET(bm::launch_gemm_tiled((const uint8_t*)act, nullptr, M, tiled, N, K, 0.0f, out,
-                                         bm::MODE_I32, s),
-                   -1);
-  return 0;
-}
-
 // ---------------------------------------------------------------------------
 // Timing and calibration helpers (no reference counterpart)
 // ---------------------------------------------------------------------------

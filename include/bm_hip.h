@@ -273,44 +273,6 @@ int bm_hip_ternary_gemm_i32_dev(const int8_t *xq,
                                 void *act,
                                 void *stream);
 
-/* A second batched product: the two-K-group GEMM on weights in an MFMA tile
- * layout (no reference counterpart: the batched products of
- * src/kernel.c:322-338 / src/arch/avx2.c:384-452 read the row-major image,
- * and so do the default products above).  Layout: for each run of 32 rows
- * and each 128-column stage, 1 KB holding the 32 rows' packed bytes of that
- * stage one after the other; rows past N are zero weights.  Tiling needs
- * K % 128 == 0 and 16-byte aligned buffers; code 11 is rewritten to 10
- * unless `canonical`. */
-size_t bm_hip_tiled_bytes(int N, int K);
-int bm_hip_tile_weights_dev(const uint8_t *packed,
-                            int N,
-                            int K,
-                            int canonical,
-                            uint8_t *tiled,
-                            void *stream);
-/* bm_hip_bitlinear_act_dev on tiled weights, bit-exact; K % 256 == 0 and
- * K <= 4096 except 3328..3840, else -2. */
-int bm_hip_bitlinear_tiled_dev(const void *act,
-                               const float *scale_x,
-                               int M,
-                               const uint8_t *tiled,
-                               int N,
-                               int K,
-                               float w_scale,
-                               float *out,
-                               void *stream);
-/* bm_hip_ternary_gemm_i32_dev on tiled weights; K % 256 == 0 and
- * K <= 16384, else -2.  `act`: bm_hip_i8_act_bytes(M, K) bytes. */
-int bm_hip_ternary_gemm_i32_tiled_dev(const int8_t *xq,
-                                      int M,
-                                      int ldx,
-                                      const uint8_t *tiled,
-                                      int N,
-                                      int K,
-                                      int32_t *out,
-                                      void *act,
-                                      void *stream);
-
 /* ------------------------------------------------------------------ */
 /* Device-resident model: the reference's model API (src/bitmamba.h:    */
 /* 282-294, src/model.c:477-1314) with weights, activations and the    */
