@@ -22,7 +22,7 @@ Prints ONE JSON line.  Legs (all by default):
             the library stream -> achieved GB/s vs 8 TB/s
   prefill   int8-MFMA GEMM at M=2048: 2048->8512 and 4096->2048, TOP/s
   cpu       the reference's own AVX2 build (oracle/_ref) on the host cores,
-            at every thread the box grants (at most 16) and at one thread,
+            at one thread fewer than the box grants (at most 15) and at one thread,
             in a child process before the GPU starts: bounded samples of the
             1B and 255M decodes, the 1024-token 1B prefill, the two M=2048
             prefill products (bitlinear_forward_batch) and the K = N = 8192
@@ -696,12 +696,50 @@ def vendor_child(reps=20):
     print(json.dumps(out), flush=True)
 
 
-def cpu_threads():
+def cpu_host():
+    """What the host grants this process and what it is: CPUs in the
+    affinity mask, CPUs of the machine, the cgroup CPU quota (cpu.max, in
+    CPUs; None when unlimited) and the CPU model."""
     try:
-        allowed = len(os.sched_getaffinity(0))
+        granted = len(os.sched_getaffinity(0))
     except AttributeError:
-        allowed = os.cpu_count() or 1
-    return max(1, min(allowed, 16))
+        granted = os.cpu_count() or 1
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = round(int(q) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for l in f:
+                if l.startswith("model name"):
+                    model = l.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(cores_granted=granted, cores_host=os.cpu_count(), cpu_quota=quota,
+                cpu_model=model)
+
+
+def cpu_threads():
+    """Pool threads of the CPU baseline: one fewer than the CPUs granted
+    (affinity mask and cgroup quota), at most 15.  The reference's pool
+    spins without yielding in its completion waits and barriers
+    (src/threadpool.c:503-507, 611-614): with as many pool threads as CPUs,
+    any other runnable thread on the box (this process, the harness) takes
+    a CPU from a pool thread and the whole pool waits for it; measured on
+    an 8-CPU host, the 1B decode's 8-thread pool makes no progress for
+    100 s beside four processes that each run 5 ms in 20, while 7 threads
+    decode at 99 tok/s beside them."""
+    h = cpu_host()
+    n = h["cores_granted"]
+    if h["cpu_quota"]:
+        n = min(n, int(h["cpu_quota"]))
+    return max(1, min(n, 16) - 1)
 
 
 def _ref_model_file(c, d):
@@ -940,8 +978,8 @@ def main():
         sys.exit(2)
     legs = set(a.legs.split(","))
     # the CPU baselines first, while this process has not started the GPU
-    # runtime (the children never touch the GPU): all host threads the box
-    # grants (at most 16), then one thread
+    # runtime (the children never touch the GPU): one thread fewer than the
+    # CPUs the box grants (at most 15), then one thread
     cpu_n = run_cpu_suite(cpu_threads()) if "cpu" in legs else {}
     cpu_1 = run_cpu_suite(1) if "cpu" in legs else {}
     cpu_stalls = cpu_n.pop("stalls", []) + cpu_1.pop("stalls", [])
@@ -952,7 +990,11 @@ def main():
                    retried=d["retried"], kind="reference",
                    sample="%d greedy steps of the same 1B-shape decode after a 7-token prefill "
                           "(reference kernels: %s, %d threads, spin-wait pool)"
-                          % (d["steps"], d["kernels"], d["threads"]))
+                          % (d["steps"], d["kernels"], d["threads"]),
+                   thread_rule="one pool thread fewer than the CPUs granted (affinity and "
+                               "cgroup quota), so that the spin-wait pool never competes with "
+                               "the bench process or the host for its last CPU")
+        cpu.update(cpu_host())
         if "decode_1b" in cpu_1:
             cpu["value_1_thread"] = cpu_1["decode_1b"]["value"]
         if cpu_stalls:
