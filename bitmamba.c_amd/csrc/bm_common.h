@@ -85,5 +85,14 @@ int dropin_blocks(int N, int K);
 hipError_t launch_dropin(const float *x, int K, const float *gamma, const uint8_t *W, int N,
                          float w_scale, float *out, float *xn, int8_t *xq, unsigned *flags,
                          unsigned seq, hipStream_t s);
+// One BitLinear call of one token on device memory in a single launch of
+// the same kernel (canonical weights): out, the int8 input xq and scale_x.
+hipError_t launch_rows_dev(const float *x, int K, const float *gamma, const uint8_t *W, int N,
+                           float w_scale, float *out, int8_t *xq, float *scale_x, hipStream_t s);
+// int8-input products with exact int32 totals, one launch, no workspace:
+// each block row (token) turns its int8 values into split nibbles itself.
+bool rows_i8_fit(int K);
+hipError_t launch_rows_i8(const int8_t *xq, int M, int ldx, int K, const uint8_t *W, int N,
+                          bool canonical, int32_t *out, hipStream_t s);
 
 }  // namespace bm

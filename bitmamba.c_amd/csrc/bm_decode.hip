@@ -525,8 +525,9 @@ __device__ __forceinline__ void lane_sums(const uint32_t (&xa)[P][16], int (&xs)
 struct DropOut {
   float* xn;        // normalized input, written by block 0 (or null)
   int8_t* xq;       // int8 input, written by block 0 (or null)
-  unsigned* flags;  // host-mapped completion words, one per block
+  unsigned* flags;  // DROP: host-mapped completion words, one per block
   unsigned seq;
+  float* scale;     // scale_x, written by block 0 (or null)
 };
 
 template <int T, int P, int NPF, int C, bool PRENORM, int MODE, int PICK, bool WP,
@@ -594,8 +595,8 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   }
 
   const Lds l = lds_carve(lds, K);
-  float* const xn_out = DROP && b == 0 ? dr.xn : nullptr;
-  int8_t* const xq_out = DROP && b == 0 ? dr.xq : nullptr;
+  float* const xn_out = b == 0 ? dr.xn : nullptr;
+  int8_t* const xq_out = b == 0 ? dr.xq : nullptr;
   float scale_x;
   if constexpr (WP) {
     if constexpr (defer_rows)
@@ -615,6 +616,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
     }
   }
   if (defer_rows && wave == 0) load_rows();
+  if (b == 0 && tid == 0 && dr.scale) *dr.scale = scale_x;
   const float inv = inv_scale_of(scale_x, w_scale);
   uint32_t xa[P][16];
   int xsl[P], xsd[P];  // slice sums (after the reduction) or lane shares (before it)
@@ -725,6 +727,152 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       part_v[blockIdx.x] = best_v;
       part_i[blockIdx.x] = best_i;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// int8-input product of one token per block row (blockIdx.y = token), exact
+// int32 totals x.w (src/kernel.c:159-316 on given int8 activations): the
+// row layout of k_rows_fused, with the token's int8 values turned into
+// split nibbles in LDS by the block itself, so there is no preparation
+// launch and no workspace; each GEMV lane subtracts its own columns' sum of
+// x (lane_sums) before the row reduction.  The token's values are loaded
+// before the weight rows (vector-memory waits complete in issue order, so
+// the conversion would otherwise wait for every weight byte).  K % 64 == 0,
+// K <= 64 T P <= 8192.
+// ---------------------------------------------------------------------------
+// 16 int8 values (bytes of d, column c = byte c) -> the split-nibble group
+// {lo4 of the even columns, lo4 of the odd, hi4 of the even, hi4 of the
+// odd}, nibble n of "even" = column 2n: byte gathers instead of per-nibble
+// shifts
+__device__ __forceinline__ uint4 split_nibbles16(uint4 d) {
+  const uint32_t L[4] = {d.x & 0x0F0F0F0Fu, d.y & 0x0F0F0F0Fu, d.z & 0x0F0F0F0Fu,
+                         d.w & 0x0F0F0F0Fu};
+  const uint32_t H[4] = {(d.x >> 4) & 0x0F0F0F0Fu, (d.y >> 4) & 0x0F0F0F0Fu,
+                         (d.z >> 4) & 0x0F0F0F0Fu, (d.w >> 4) & 0x0F0F0F0Fu};
+  // bytes {a.b0, a.b2, b.b0, b.b2} (even) or {a.b1, a.b3, b.b1, b.b3} (odd),
+  // then byte pairs merged into nibble pairs and the merged bytes gathered
+  auto pack = [](const uint32_t (&v)[4], uint32_t sel) __attribute__((always_inline)) {
+    const uint32_t e01 = __builtin_amdgcn_perm(v[1], v[0], sel);
+    const uint32_t e23 = __builtin_amdgcn_perm(v[3], v[2], sel);
+    const uint32_t t01 = e01 | (e01 >> 4), t23 = e23 | (e23 >> 4);
+    return __builtin_amdgcn_perm(t23, t01, 0x06040200u);
+  };
+  // v_perm_b32 selector bytes: 0..3 = bytes of the second operand, 4..7 of
+  // the first
+  return make_uint4(pack(L, 0x06040200u), pack(L, 0x07050301u), pack(H, 0x06040200u),
+                    pack(H, 0x07050301u));
+}
+
+__device__ __forceinline__ int dot64c(uint4 w, const uint32_t (&xa)[16]) {
+  return dot64(make_uint4(canon_codes(w.x), canon_codes(w.y), canon_codes(w.z), canon_codes(w.w)),
+               xa);
+}
+
+template <int T, int P, int NPF, bool CANON>
+__global__ __launch_bounds__(256) void k_rows_i8(const int8_t* __restrict__ xq, int ldx, int K,
+                                                 const uint8_t* __restrict__ W, int N,
+                                                 int32_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t nib[];  // [K / 4]
+  constexpr int RPW = 64 / T;
+  constexpr int XG = 2;  // 16-column groups per thread: K / 16 <= 512
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int u = lane % T, sub = lane / T, unit_base = sub * T;
+  const int G = (N + RPW - 1) / RPW;
+  const int per = G / (int)gridDim.x, extra = G % (int)gridDim.x, b = blockIdx.x;
+  const int g0 = b * per + min(b, extra);
+  const int g1 = g0 + per + (b < extra ? 1 : 0);
+  const int m = blockIdx.y;
+  const size_t wstride = (size_t)(K >> 2);
+  const int chunks = K >> 6, n_groups = K >> 4;
+
+  // the token's int8 values first (16 columns per group)
+  const int8_t* __restrict__ xr = xq + (size_t)m * ldx;
+  const bool vec = ((uintptr_t)xr & 15) == 0;
+  uint4 xv[XG];
+#pragma unroll
+  for (int i = 0; i < XG; ++i) {
+    const int g = tid + i * (int)blockDim.x;
+    xv[i] = make_uint4(0, 0, 0, 0);
+    if (g < n_groups) {
+      if (vec) {
+        xv[i] = *(const uint4*)(xr + 16 * g);
+      } else {
+        uint32_t wd[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) wd[j >> 2] |= (uint32_t)(uint8_t)xr[16 * g + j] << (8 * (j & 3));
+        xv[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+      }
+    }
+  }
+
+  uint4 wv[NPF][P];
+#pragma unroll
+  for (int it = 0; it < NPF; ++it) {
+    const int grp = g0 + wave + 4 * it;
+    const int r = grp * RPW + sub;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = p * T + u;
+      wv[it][p] = (grp < g1 && r < N && j < chunks)
+                      ? load_stream16(W + (size_t)r * wstride + 16 * j)
+                      : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // split nibbles of the token's values into LDS
+#pragma unroll
+  for (int i = 0; i < XG; ++i) {
+    const int g = tid + i * (int)blockDim.x;
+    if (g < n_groups) *(uint4*)(nib + 4 * g) = split_nibbles16(xv[i]);
+  }
+  __syncthreads();
+
+  uint32_t xa[P][16];
+  int xsd[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int j = p * T + u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint4 v = j < chunks ? *(const uint4*)(nib + 16 * j + 4 * g) : make_uint4(0, 0, 0, 0);
+      xa[p][4 * g + 0] = v.x;
+      xa[p][4 * g + 1] = v.y;
+      xa[p][4 * g + 2] = v.z;
+      xa[p][4 * g + 3] = v.w;
+    }
+  }
+  lane_sums<P>(xa, xsd);
+
+  // int32 totals: the lane's passes first, then one row reduction
+  auto total = [&](const uint4 (&w)[P]) __attribute__((always_inline)) {
+    int part = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      part += (CANON ? dot64(w[p], xa[p]) : dot64c(w[p], xa[p])) - xsd[p];
+    return row_total_i32<T>(part, 0, unit_base);
+  };
+  int32_t* __restrict__ orow = out + (size_t)m * N;
+#pragma unroll
+  for (int it = 0; it < NPF; ++it) {
+    const int grp = g0 + wave + 4 * it;
+    if (grp < g1) {  // uniform per wave
+      const int t = total(wv[it]);
+      const int r = grp * RPW + sub;
+      if (u == 0 && r < N) orow[r] = t;
+    }
+  }
+  for (int grp = g0 + wave + 4 * NPF; grp < g1; grp += 4) {  // beyond the prefetch
+    const int r = grp * RPW + sub;
+    uint4 w[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int j = p * T + u;
+      w[p] = (r < N && j < chunks) ? load_stream16(W + (size_t)r * wstride + 16 * j)
+                                   : make_uint4(0, 0, 0, 0);
+    }
+    const int t = total(w);
+    if (u == 0 && r < N) orow[r] = t;
   }
 }
 
@@ -1067,7 +1215,42 @@ hipError_t launch_dropin(const float* x, int K, const float* gamma, const uint8_
                          unsigned seq, hipStream_t s) {
   if (!rows_fit(K) || N < 1) return hipErrorInvalidValue;
   return rows_t<4, false, 0, 0, true>(x, K, nullptr, gamma, W, N, w_scale, out, nullptr, nullptr,
-                                      s, 1.0f, DropOut{xn, xq, flags, seq});
+                                      s, 1.0f, DropOut{xn, xq, flags, seq, nullptr});
+}
+
+hipError_t launch_rows_dev(const float* x, int K, const float* gamma, const uint8_t* W, int N,
+                           float w_scale, float* out, int8_t* xq, float* scale_x, hipStream_t s) {
+  if (!rows_fit(K) || N < 1) return hipErrorInvalidValue;
+  return rows_t<4, false, 0, 0>(x, K, nullptr, gamma, W, N, w_scale, out, nullptr, nullptr, s,
+                                1.0f, DropOut{nullptr, xq, nullptr, 0, scale_x});
+}
+
+bool rows_i8_fit(int K) { return K % 64 == 0 && K <= 8192; }  // K / 16 <= 2 * 256 groups
+
+template <int T, int P, int NPF>
+static hipError_t rows_i8_t(const int8_t* xq, int M, int ldx, int K, const uint8_t* W, int N,
+                            bool canonical, int32_t* out, hipStream_t s) {
+  const int rpw = 64 / T;
+  const int G = (N + rpw - 1) / rpw;
+  const dim3 grid((unsigned)max(1, (G + 4 * NPF - 1) / (4 * NPF)), (unsigned)M), block(256);
+  const size_t lds = (size_t)K;  // K / 4 dwords of split nibbles
+  if (canonical)
+    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, true>), grid, block, lds, s, xq, ldx, K, W, N, out);
+  else
+    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, false>), grid, block, lds, s, xq, ldx, K, W, N, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_i8(const int8_t* xq, int M, int ldx, int K, const uint8_t* W, int N,
+                          bool canonical, int32_t* out, hipStream_t s) {
+  if (!rows_i8_fit(K) || N < 1 || M < 1) return hipErrorInvalidValue;
+  if (K <= 1024) return rows_i8_t<16, 1, 4>(xq, M, ldx, K, W, N, canonical, out, s);
+  if (K <= 2048) return rows_i8_t<32, 1, 4>(xq, M, ldx, K, W, N, canonical, out, s);
+  if (K <= 4096) return rows_i8_t<64, 1, 4>(xq, M, ldx, K, W, N, canonical, out, s);
+  // K = N = 8192, M = 1 (stress shape, weights cold): 6.5 us with two row
+  // groups per wave (1024 blocks), 7.1 with four, 7.7 with eight, 7.5 with
+  // 32 lanes per row
+  return rows_i8_t<64, 2, 2>(xq, M, ldx, K, W, N, canonical, out, s);
 }
 
 // in_proj + SSM for every head: y (and the states) updated in one launch

@@ -627,6 +627,14 @@ extern "C" int bm_hip_bitlinear_dev(const float* x, int M, int K, const float* n
     bm_set_error("bitlinear: act workspace required");
     return -2;
   }
+  if (M == 1 && canonical && bm::rows_fit(K)) {
+    // one token: the fused single-launch kernel of the decode (RMSNorm and
+    // int8 prologue in every block, block 0 writing x_quant and scale_x)
+    BM_HIP_CHECK_RET(bm::launch_rows_dev(x, K, norm_w, packed, N, w_scale, out, x_quant, scale_x,
+                                         s),
+                     -1);
+    return 0;
+  }
   BM_HIP_CHECK_RET(bm::launch_quantize(x, M, K, K, norm_w, nullptr, x_quant, quant_stride, scale_x,
                                        generic ? nullptr : (uint8_t*)act, s),
                    -1);
@@ -659,6 +667,12 @@ extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
   if (!act) {
     bm_set_error("ternary_gemm_i32: act workspace required");
     return -2;
+  }
+  if (M == 1 && bm::rows_i8_fit(K)) {
+    // one token: one launch, the block turns the int8 row into split
+    // nibbles itself (the workspace stays unused)
+    BM_HIP_CHECK_RET(bm::launch_rows_i8(xq, M, ldx, K, packed, N, canonical != 0, out, s), -1);
+    return 0;
   }
   BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act,
                                       bm::product_reads_nibbles(M, N, K), s),

@@ -220,7 +220,9 @@ int bm_hip_bitlinear_act_dev(const void *act,
                              void *stream);
 
 /* Quantize + product in one call (device pointers): scalar_bitlinear_
- * forward_batch semantics for M tokens. `act` as above. */
+ * forward_batch semantics for M tokens. `act` as above.  One token on
+ * canonical weights (K % 64 == 0, K <= 8192) runs as a single launch that
+ * leaves `act` untouched. */
 int bm_hip_bitlinear_dev(const float *x,
                          int M,
                          int K,
@@ -259,8 +261,9 @@ size_t bm_hip_noalloc_scratch_bytes(void);
 
 /* Exact int32 product of int8 activations and ternary weights:
  * out[m*N + r] = sum_k xq[m*ldx + k] * decode(W[r][k]) (stress shape;
- * activations need no quantization).  M = 1 runs the decode GEMV, larger M
- * the int8 MFMA GEMM.  Needs bm_hip_i8_act_bytes(M, K) bytes of `act`. */
+ * activations need no quantization).  M = 1 (K % 64 == 0, K <= 8192) runs
+ * as one GEMV launch that reads xq itself and leaves `act` untouched; larger
+ * M the int8 MFMA GEMM.  Needs bm_hip_i8_act_bytes(M, K) bytes of `act`. */
 size_t bm_hip_i8_act_bytes(int M, int K);
 int bm_hip_ternary_gemm_i32_dev(const int8_t *xq,
                                 int M,

@@ -337,6 +337,33 @@ def test_bitlinear_fp32_exact(hip, M, K, N):
     same_bits(out, ref, "out")
 
 
+@pytest.mark.parametrize("K,N", [(1024, 4384), (2048, 8384), (4096, 2048), (8192, 1000),
+                                 (1088, 300), (3072, 130), (5120, 64), (64, 7)])
+def test_bitlinear_dev_one_token_fused(hip, K, N):
+    """bm_hip_bitlinear_dev at one token on canonical weights (one launch of
+    the decode's fused kernel, every block running the RMSNorm/int8
+    prologue, block 0 writing x_quant and scale_x): out, x_quant and
+    scale_x bit-exact against the oracle."""
+    note("bitlinear_dev one token K=%d N=%d" % (K, N))
+    r = rnd(7 * K + N)
+    packed = bh.synth_ternary(K, N, N, K, bh.SYNTH_UNIFORM)
+    x = r.standard_normal((1, K)).astype(np.float32)
+    x[:, r.integers(0, K, 3)] *= 10.0
+    g = (r.standard_normal(K) * 0.02).astype(np.float32)
+    dx, dg, dw = DB.from_array(x), DB.from_array(g), DB.from_array(packed)
+    do, dq, ds = DB(4 * N), DB(K), DB(4)
+    da = DB(hip.bm_hip_act_bytes(1, K))
+    bh.check(hip.bm_hip_bitlinear_dev(dx.ptr, 1, K, dg.ptr, dw.ptr, N, 0.02, 1, do.ptr, dq.ptr,
+                                      K, ds.ptr, da.ptr, None), "bitlinear_dev")
+    hip.bm_hip_synchronize()
+    ref, _, rq = native.orc_bitlinear(x, packed, N, K, 0.02, g)
+    _, oq, osc, _ = native.orc_quantize_rows(x, g)
+    np.testing.assert_array_equal(dq.download((1, K), np.int8), rq)
+    np.testing.assert_array_equal(dq.download((1, K), np.int8), oq)
+    same_bits(ds.download(1, np.float32), osc.astype(np.float32), "scale_x")
+    same_bits(do.download((1, N), np.float32), ref, "out")
+
+
 def test_prefill_shapes_sampled(hip):
     """Prefill GEMM shapes M=2048: K=2048->N=8512 and K=4096->N=2048 (and
     M=1233, 1024 of the 1B prefill, which take the other tile shapes), fp32,
