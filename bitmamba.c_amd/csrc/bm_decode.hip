@@ -516,11 +516,12 @@ __device__ __forceinline__ void lane_sums(const uint32_t (&xa)[P][16], int (&xs)
 //               max of what it stored under `x > m` from -1e30f
 //   DROP:    a single call on mapped host memory (x in, out, and block 0's
 //            copies of the normalized and int8 input out): each block
-//            stages its rows in LDS, writes them as one contiguous run and
-//            then writes dr.seq to its own host-mapped word dr.flags[block],
-//            which the caller polls instead of synchronizing the stream (no
-//            device-wide counter: atomics on one word serialize across the
-//            XCDs, ~70 ns per block)
+//            stages its rows in LDS, writes them as one contiguous run of
+//            write-through stores and then writes dr.seq to its own
+//            host-mapped word dr.flags[block], which the caller polls
+//            instead of synchronizing the stream (no device-wide counter:
+//            atomics on one word serialize across the XCDs, ~70 ns per
+//            block; system-scope atomics on a host word, ~1 us each)
 // ---------------------------------------------------------------------------
 struct DropOut {
   float* xn;        // normalized input, written by block 0 (or null)
@@ -677,14 +678,22 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   if constexpr (DROP) {
     __syncthreads();
     const int r_end = min(g1 * RPW, N);
-    for (int r = r0 + tid; r < r_end; r += blockDim.x) out[r] = l.sq[r - r0];
+    // system-scope stores go through to host memory (nothing of them stays
+    // in L2), so each thread only waits for its own stores to complete
+    // before the barrier; an L2 write-back per wave (a system release
+    // fence) costs ~35 ns per block at 786 blocks.  A barrier alone does
+    // not wait for the other waves' stores.  Block 0 also wrote the copies
+    // of the input with plain stores in the prologue: its threads take the
+    // full release fence.
+    for (int r = r0 + tid; r < r_end; r += blockDim.x)
+      __hip_atomic_store(out + r, l.sq[r - r0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (b == 0)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+    else
+      __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (tid == 0) {
-      // the block's stores (and block 0's copies) reach the host before
-      // its completion word does
-      __threadfence_system();
+    if (tid == 0)
       __hip_atomic_store(dr.flags + b, dr.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
   }
 
   if constexpr (PICK == 2) {

@@ -10,6 +10,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <immintrin.h>
+
 #include <chrono>
 #include <mutex>
 #include <unordered_map>
@@ -82,13 +84,9 @@ struct Backend {
   unsigned seq = 0;
 };
 
-// completion words of the one-launch path: one per block.  Every block of
-// that kernel reads the whole input vector over the bus, so it is used only
-// up to this many blocks: measured at one token, K = 1024 -> N = 4192 (66
-// blocks) takes 19.4 us against 24.0 us for quantize + product + stream
-// synchronization, K = 2048 -> N = 8384 (262 blocks) 26.8 against 26.9 us,
-// and K = 1024 -> N = 50257 (786 blocks) 42.4 against 33.9 us
-constexpr int kDropInMaxBlocks = 320;
+// completion words of the one-launch path: one per block, which covers
+// the 50257-row LM heads (786 blocks at K = 1024, 1571 at K = 2048)
+constexpr int kDropInMaxBlocks = 2048;
 
 Backend& B() {
   static Backend* b = new Backend();  // intentionally leaked: no static dtor
@@ -170,26 +168,58 @@ unsigned next_seq(Backend& b) {
   return b.seq;
 }
 
-// Waits until every block of the one-launch kernel has published `seq`:
-// polls the mapped words in block order (a stream synchronization costs
-// ~5 us more than the kernel's own completion writes take to arrive).
-// After ~2 s of polling it falls back to synchronizing the stream, which
-// reports a failed kernel.
-hipError_t wait_flags(const volatile unsigned* flags, int n, unsigned seq, hipStream_t s) {
-  const auto t0 = std::chrono::steady_clock::now();
-  int k = 0;
-  for (unsigned i = 1; k < n; ++i) {
-    while (k < n && __atomic_load_n(flags + k, __ATOMIC_ACQUIRE) == seq) ++k;
-    if (k < n && (i & 4095) == 0 &&
-        std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2))
-      break;
+// Whether words[0..n) all hold seq.  The CPU reads mapped coherent memory
+// without caching it (~30 ns per load whatever its width), so the words
+// are compared 8 (AVX2) or 4 (SSE2) per load: 786 words take ~3 us instead
+// of ~23 us one by one.
+__attribute__((target("avx2"))) bool all_published_avx2(const unsigned* w, int n, unsigned seq) {
+  const __m256i want = _mm256_set1_epi32((int)seq);
+  int i = 0;
+  for (; i + 8 <= n; i += 8) {
+    const __m256i v = _mm256_load_si256((const __m256i*)(w + i));
+    if (_mm256_movemask_epi8(_mm256_cmpeq_epi32(v, want)) != -1) return false;
   }
-  if (k == n) return hipSuccess;
+  for (; i < n; ++i)
+    if (__atomic_load_n(w + i, __ATOMIC_ACQUIRE) != seq) return false;
+  return true;
+}
+
+bool all_published_sse2(const unsigned* w, int n, unsigned seq) {
+  const __m128i want = _mm_set1_epi32((int)seq);
+  int i = 0;
+  for (; i + 4 <= n; i += 4) {
+    const __m128i v = _mm_load_si128((const __m128i*)(w + i));
+    if (_mm_movemask_epi8(_mm_cmpeq_epi32(v, want)) != 0xffff) return false;
+  }
+  for (; i < n; ++i)
+    if (__atomic_load_n(w + i, __ATOMIC_ACQUIRE) != seq) return false;
+  return true;
+}
+
+bool all_published(const unsigned* w, int n, unsigned seq) {
+  static const bool avx2 = __builtin_cpu_supports("avx2");
+  const bool r = avx2 ? all_published_avx2(w, n, seq) : all_published_sse2(w, n, seq);
+  __atomic_thread_fence(__ATOMIC_ACQUIRE);  // the results are read after the words
+  return r;
+}
+
+// Waits until every block of the one-launch kernel has published `seq` (a
+// stream synchronization costs ~5 us more than the kernel's own completion
+// writes take to arrive): the blocks finish about in launch order, so the
+// last block's word is polled alone, then all words are checked with wide
+// loads.  After ~2 s of polling it falls back to synchronizing the stream,
+// which reports a failed kernel.
+hipError_t wait_flags(const unsigned* flags, int n, unsigned seq, hipStream_t s) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (unsigned i = 1;; ++i) {
+    if (__atomic_load_n(flags + n - 1, __ATOMIC_ACQUIRE) == seq && all_published(flags, n, seq))
+      return hipSuccess;
+    if ((i & 4095) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) break;
+  }
   const hipError_t e = hipStreamSynchronize(s);
   if (e != hipSuccess) return e;
-  while (k < n && __atomic_load_n(flags + k, __ATOMIC_ACQUIRE) == seq) ++k;
-  if (k == n) return hipSuccess;
-  bm_set_error("one-launch BitLinear finished without publishing block %d's completion word", k);
+  if (all_published(flags, n, seq)) return hipSuccess;
+  bm_set_error("one-launch BitLinear finished without publishing every block's completion word");
   return hipErrorUnknown;
 }
 
@@ -335,7 +365,7 @@ void host_bitlinear(const float* x, int M, int n, const uint8_t* packed, int row
     if (e == hipSuccess)
       e = bm::launch_dropin(dx, n, dG, dW, rows, w_scale, (float*)dio, (float*)(dio + o_norm),
                             (int8_t*)(dio + o_q), (unsigned*)b.h_flag.dev, seq, s);
-    if (e == hipSuccess) e = wait_flags((const volatile unsigned*)b.h_flag.ptr, nblk, seq, s);
+    if (e == hipSuccess) e = wait_flags((const unsigned*)b.h_flag.ptr, nblk, seq, s);
   } else {
     if (e == hipSuccess)
       e = bm::launch_quantize(dx, M, n, n, dG, (float*)(dio + o_norm), (int8_t*)(dio + o_q), n,

@@ -455,12 +455,13 @@ def _dropin_ref(x, packed, N, K, scale, g):
 
 
 # one token: the single-launch path (K % 64 == 0, outputs within the mapped
-# buffer, at most 320 blocks) and the two-launch path (K = 1000, the
-# 50257-row products, and an output too large for the mapped buffer); calls
-# alternate shapes so that each one must see its own completion words
+# buffer, at most 2048 blocks: the 50257-row LM heads take 786 and 1571)
+# and the two-launch path (K = 1000, and an output too large for the mapped
+# buffer); calls alternate shapes so that each one must see its own
+# completion words
 DROPIN_SHAPES = [(64, 1), (128, 3), (1024, 4192), (1000, 77), (1536, 65), (2048, 8384),
                  (3072, 130), (4096, 2048), (8192, 300), (2048, 50257), (1024, 70000),
-                 (64, 2), (1024, 4384)]
+                 (64, 2), (1024, 50257), (1024, 4384)]
 
 
 def test_dropin_single_token_shapes(hip):
