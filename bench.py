@@ -230,6 +230,99 @@ def leg_d255m(L, fast=False):
     return r
 
 
+def _dropin_run(L, R, native, path, c, threads, kind, hip):
+    """One greedy decode of config c through the reference's own
+    model_prefill / model_forward_step, its CPU table of `kind` (0 scalar,
+    1 the dispatch_init choice: AVX2) at `threads` pool threads, with the
+    BitLinear / RMSNorm entries handed to this library when `hip`."""
+    name = R.bmref_init(threads, kind).decode()
+    R.bmref_set_poll(100)
+    h = R.bmref_model_load(path.encode())
+    if not h:
+        raise RuntimeError("reference model_load failed")
+    try:
+        if hip:
+            addr, size = C.c_void_p(), C.c_size_t()
+            if not R.bmref_model_image(h, C.byref(addr), C.byref(size)):
+                raise RuntimeError("reference model not mapped")
+            if not L.bm_hip_set_mmap(addr, size.value):
+                raise RuntimeError("bm_hip_set_mmap: " + bh.last_error())
+            if R.bmref_use_hip(C.cast(L.bm_hip_register, C.c_void_p)) != 1:
+                raise RuntimeError("bm_hip_register refused the table")
+            name = "%s + hip" % name
+        what = "drop-in 255M [%s]" % name
+        beat("%s: model loaded" % what)
+        prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
+        p = np.ascontiguousarray(prompt[:-1], np.int32)
+        t0 = time.perf_counter()
+        R.bmref_model_prefill(h, native.ptr(p), p.size)
+        pf_ms = (time.perf_counter() - t0) * 1e3
+        beat("%s: prompt prefilled (%.1f ms)" % (what, pf_ms))
+        hist, cur = [int(t) for t in prompt], int(prompt[-1])
+        toks, times = [], []
+        for _ in range(c["steps"]):
+            harr = np.array(hist[-256:], np.int32)
+            t0 = time.perf_counter()
+            cur = R.bmref_model_step(h, cur, native.ptr(harr), harr.size, 1.0)
+            times.append(time.perf_counter() - t0)
+            toks.append(int(cur))
+            hist.append(cur)
+            if len(toks) % 32 == 0:
+                beat("%s: step %d %.3f ms" % (what, len(toks), times[-1] * 1e3))
+    finally:
+        R.bmref_model_free(h)
+    t = np.array(times)
+    return toks, dict(tok_s=round(len(t) / t.sum(), 1), ms_per_step=round(t.mean() * 1e3, 4),
+                      median_ms_per_step=round(float(np.median(t)) * 1e3, 4),
+                      prefill_ms=round(pf_ms, 2), kernels=name, threads=threads)
+
+
+def leg_dropin_255m(L, threads):
+    """The drop-in as a user of the reference runs it: the reference's own
+    model_load / model_prefill / model_forward_step (oracle/_ref, built from
+    its sources, with its spin-wait thread pool) with its plugin table handed
+    to bm_hip_register after bm_hip_set_mmap registered the mapped model
+    file (src/dispatch.c:15-52, src/model.c:840-851): every BitLinear (48
+    per token plus the LM head) and the final RMSNorm run through this
+    library, one launch each, while ssm_inner, the embedding and the sampler
+    stay on the CPU.  128 greedy steps of the 255M shape, three runs:
+      value: the reference's AVX2 table (its ssm_inner) + this library;
+      cpu_same_kernels: the same reference, all on its AVX2 table (its AVX2
+        BitLinear differs from its own scalar kernel, which this library
+        reproduces, in the last bit of most outputs, so the two streams
+        drift apart: first_divergence says where);
+      scalar_ssm: the scalar table + this library, whose tokens must be the
+        scalar reference's stream (tests/golden/stream_255m.json).
+    The pool gets one thread fewer than the CPU baseline's: this process's
+    main thread also spins (it polls the GPU's completion words), and a
+    spin-wait pool that shares its last CPU stalls (see cpu_threads)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import native
+    c = CFG_255M
+    R = native.ref()
+    gold_path = os.path.join(ROOT, "tests", "golden", "stream_255m.json")
+    gold = json.load(open(gold_path)) if os.path.exists(gold_path) else None
+    try:
+        with tempfile.TemporaryDirectory(dir=tempfile.gettempdir()) as d:
+            path = _ref_model_file(c, d)
+            beat("drop-in 255M: model file written")
+            toks, r = _dropin_run(L, R, native, path, c, threads, 1, True)
+            ctoks, cr = _dropin_run(L, R, native, path, c, threads, 1, False)
+            stoks, sr = _dropin_run(L, R, native, path, c, threads, 0, True)
+    finally:
+        R.bmref_shutdown()
+    div = next((i for i, (a, b) in enumerate(zip(toks, ctoks)) if a != b), None)
+    r.update(steps=c["steps"],
+             tokens_match_cpu_same_kernels=toks == ctoks, first_divergence_from_cpu=div,
+             cpu_same_kernels=cr,
+             scalar_ssm=dict(sr, tokens_match_reference=(stoks == gold["tokens"]) if gold
+                             else None),
+             calls_per_token="48 BitLinear (in_proj 1024->4192, out_proj 2048->1024) + LM "
+                             "head 1024->50257 + final RMSNorm on the GPU; ssm_inner on "
+                             "the CPU")
+    return r
+
+
 def leg_fast_quant(L, M=4096):
     """Fast against parity quantization on the same rows (the parity kernel
     is bit-exact with the reference's scalar quantizer): int8 mismatch rate,
@@ -896,6 +989,92 @@ def cpu_child(threads, budget_s):
     R.bmref_shutdown()
 
 
+def thread_states(pid):
+    """State, kernel wait channel and CPU time of each thread of a process
+    (from /proc, no tracing): how a stalled child was stalled."""
+    out = {}
+    try:
+        for tid in sorted(os.listdir("/proc/%d/task" % pid), key=int):
+            base = "/proc/%d/task/%s/" % (pid, tid)
+            try:
+                comm = open(base + "comm").read().strip()
+                st = open(base + "stat").read()
+                f = st[st.rindex(")") + 2:].split()
+                wchan = open(base + "wchan").read().strip() if os.path.exists(base + "wchan") \
+                    else "?"
+                key = "%s%s %s %s" % ("main:" if int(tid) == pid else "", comm, f[0], wchan)
+                d = out.setdefault(key, dict(n=0, cpu_ticks=0))
+                d["n"] += 1
+                d["cpu_ticks"] += int(f[11]) + int(f[12])
+            except (OSError, ValueError, IndexError):
+                continue
+    except OSError:
+        pass
+    return out
+
+
+def dropin_child(threads):
+    """The drop-in decode leg in a process of its own (its spin-wait pool
+    never shares a process with the other legs); prints "DROPIN {json}"."""
+    L = bh.lib()
+    if not L.bm_hip_init():
+        sys.exit("bm_hip_init: " + bh.last_error())
+    print("DROPIN " + json.dumps(leg_dropin_255m(L, threads)), flush=True)
+
+
+def run_dropin(threads, stall_s=60.0, total_s=300.0):
+    """dropin_child, watched like the CPU suite: a child that prints nothing
+    for stall_s is killed and run again once with half the threads; the
+    result records the stalls."""
+    import subprocess
+    import threading
+    stalls = []
+    start = time.time()
+    for t in (threads, max(1, threads // 2)):
+        cmd = [sys.executable, os.path.abspath(__file__), "--dropin-child", str(t)]
+        # one OpenMP thread: the child's only OpenMP work is writing the
+        # synthetic model file, and an idle 16-thread OpenMP pool beside
+        # the reference's pool and the HIP runtime's threads was followed
+        # by a pool worker that never started (thread_states)
+        env = dict(os.environ, OMP_NUM_THREADS="1")
+        proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, text=True, bufsize=1, env=env)
+        lines, last = [], [time.time()]
+
+        def read(f=proc.stdout, lines=lines, last=last):
+            for l in f:
+                lines.append(l)
+                last[0] = time.time()
+
+        rd = threading.Thread(target=read, daemon=True)
+        rd.start()
+        killed = False
+        threads_seen = None
+        while proc.poll() is None:
+            time.sleep(0.2)
+            if time.time() - last[0] > stall_s or time.time() - start > total_s:
+                threads_seen = thread_states(proc.pid)
+                proc.kill()
+                killed = True
+                proc.wait()
+        rd.join(5)
+        if threads_seen:
+            log("drop-in: stalled child's threads: %s" % json.dumps(threads_seen))
+        for l in lines:
+            if l.startswith("DROPIN "):
+                d = json.loads(l[7:])
+                if stalls:
+                    d["stalls"] = stalls
+                return d
+        where = [l[2:].strip() for l in lines if l.startswith("P ")]
+        stalls.append(dict(threads=t, after=where[-1] if where else "start",
+                           stopped="no output for %ds" % stall_s if killed
+                           else "rc %s" % proc.returncode))
+        log("drop-in: child with %d threads stopped: %s" % (t, json.dumps(stalls[-1])))
+        if time.time() - start > total_s:
+            break
+    return dict(tok_s=None, stalls=stalls)
+
+
 def run_cpu_suite(threads, stall_s=20.0, total_s=240.0):
     """The CPU baseline legs in a child process, watched: a child that
     prints nothing for stall_s is killed and run again (same thread count
@@ -958,6 +1137,9 @@ def main():
     if len(sys.argv) == 4 and sys.argv[1] == "--cpu-child":
         cpu_child(int(sys.argv[2]), float(sys.argv[3]))
         return
+    if len(sys.argv) == 3 and sys.argv[1] == "--dropin-child":
+        dropin_child(int(sys.argv[2]))
+        return
     if len(sys.argv) == 2 and sys.argv[1] == "--vendor-child":
         vendor_child()
         return
@@ -970,7 +1152,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--legs",
                     default="decode,sampled,fast,roofline,mfma,prefill,d255m,gemv1,stress,vendor,"
-                            "cpu")
+                            "dropin,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: the BitLinear hot path runs on exactly one GPU (there is no "
@@ -1048,6 +1230,10 @@ def main():
     cpy = leg_copy(L) if "copy" in legs else None
     if cpy:
         log("copy: %s" % json.dumps(cpy))
+    # in a child process: it starts the reference's spin-wait pool
+    dropin = run_dropin(max(1, cpu_threads() - 1)) if "dropin" in legs else None
+    if dropin:
+        log("drop-in decode 255M: %s" % json.dumps(dropin))
 
     bpt = packed_bytes_per_token(CFG_1B)
     line = {"metric": METRIC, "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -1076,6 +1262,8 @@ def main():
             res["prefill_model"]["cpu"] = cpu_of("prefill_1b")
         if d255:
             d255["cpu"] = cpu_of("decode_255m")
+        if dropin:
+            dropin["cpu"] = cpu_of("decode_255m")
         if pre:
             for k in pre:
                 pre[k]["cpu"] = cpu_of("gemm_" + k)
@@ -1093,6 +1281,7 @@ def main():
     line["mfma_ceiling"] = mf
     line["prefill_gemm"] = pre
     line["decode_255m"] = d255
+    line["dropin_decode_255m"] = dropin
     line["bitlinear_k1024_n4384"] = g1
     line["stress_k8192_n8192"] = strs
     line["vendor_int8_gemm"] = vend

@@ -74,6 +74,10 @@ hipError_t launch_rms_norm(const float *x, int n, const float *gamma,
                            float *out, float *max_out, hipStream_t s);
 hipError_t launch_canonicalize(uint8_t *p, size_t bytes, hipStream_t s);
 
+// Host -> device copy of caller memory through the library's own pinned
+// staging (bm_runtime.hip); enqueued on s, complete once s is.
+hipError_t upload(void *dst, const void *src, size_t bytes, hipStream_t s);
+
 // One BitLinear call (RMSNorm + int8 + GEMV, canonical weights) on mapped
 // host memory in a single launch of dropin_blocks(N, K) blocks
 // (bm_decode.hip): x, out, and the copies xn (normalized input) and xq

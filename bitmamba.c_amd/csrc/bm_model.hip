@@ -665,13 +665,13 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
   };
   auto put_f = [&](const bm_bit2_tensor_t* t, size_t count) -> float* {
     float* d = (float*)take(count * 4);
-    if (hipMemcpy(d, t->data, count * 4, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    if (bm::upload(d, t->data, count * 4, m->stream) != hipSuccess) return nullptr;
     return d;
   };
   auto put_w = [&](const bm_bit2_tensor_t* t) -> uint8_t* {
     const size_t b = packed_bytes(t);
     uint8_t* d = take(b);
-    if (hipMemcpy(d, t->packed, b, hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    if (bm::upload(d, t->packed, b, m->stream) != hipSuccess) return nullptr;
     if (bm::launch_canonicalize(d, b, m->stream) != hipSuccess) return nullptr;
     return d;
   };
@@ -691,7 +691,7 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
       memcpy(dst + (2 * hd + 2) * rb, t->packed + (size_t)(2 * di + 2 * nh + h) * rb, rb);
     }
     uint8_t* d = take(perm.size());
-    if (hipMemcpy(d, perm.data(), perm.size(), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    if (bm::upload(d, perm.data(), perm.size(), m->stream) != hipSuccess) return nullptr;
     if (bm::launch_canonicalize(d, perm.size(), m->stream) != hipSuccess) return nullptr;
     if (hipStreamSynchronize(m->stream) != hipSuccess) return nullptr;
     return d;
@@ -726,7 +726,7 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
     MCHECK(hipMemcpy(Ly.conv_wt, wt.data(), (size_t)4 * di * 4, hipMemcpyHostToDevice));
     Ly.conv_b = put_f(&t[BM_L_CONV_B], di);
     Ly.dt_bias = put_f(&t[BM_L_DT_BIAS], nh);
-    MCHECK(hipMemcpy(alog, t[BM_L_A_LOG].data, (size_t)nh * 4, hipMemcpyHostToDevice));
+    MCHECK(bm::upload(alog, t[BM_L_A_LOG].data, (size_t)nh * 4, m->stream));
     Ly.A = (float*)take((size_t)nh * 4);
     hipLaunchKernelGGL(bm::k_neg_exp, dim3((nh + 255) / 256), dim3(256), 0, m->stream, alog,
                        Ly.A, nh);

@@ -247,6 +247,56 @@ bool init_locked(Backend& b) {
   return true;
 }
 
+}  // namespace
+
+namespace bm {
+
+// Host -> device copies of caller memory go through pinned staging of the
+// library's own (two 4 MiB halves used in turn, each reused once the copy
+// out of it has completed): the runtime then never pins, registers or
+// tracks the caller's pages, which may be a mapped model file that other
+// threads of the caller read at the same time, and the source may be
+// reused as soon as the call returns.
+hipError_t upload(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  constexpr size_t kHalf = (size_t)4 << 20;
+  static std::mutex mu;
+  static uint8_t* stage = nullptr;
+  static hipEvent_t done[2];
+  static bool pending[2];
+  std::lock_guard<std::mutex> lk(mu);
+  if (!stage) {
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, 2 * kHalf, hipHostMallocDefault);
+    if (e != hipSuccess) return e;
+    for (int k = 0; k < 2; ++k) {
+      e = hipEventCreateWithFlags(&done[k], hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+      pending[k] = false;
+    }
+    stage = (uint8_t*)p;
+  }
+  int k = 0;
+  for (size_t off = 0; off < bytes; off += kHalf, k ^= 1) {
+    const size_t n = bytes - off < kHalf ? bytes - off : kHalf;
+    if (pending[k]) {
+      const hipError_t e = hipEventSynchronize(done[k]);
+      if (e != hipSuccess) return e;
+      pending[k] = false;
+    }
+    memcpy(stage + k * kHalf, (const uint8_t*)src + off, n);
+    hipError_t e = hipMemcpyAsync((uint8_t*)dst + off, stage + k * kHalf, n,
+                                  hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipEventRecord(done[k], s);
+    if (e != hipSuccess) return e;
+    pending[k] = true;
+  }
+  return hipSuccess;
+}
+
+}  // namespace bm
+
+namespace {
+
 // Copies a packed tensor to an aligned device buffer and rewrites code 11.
 const uint8_t* register_packed(Backend& b, const uint8_t* host, size_t bytes) {
   auto it = b.packed.find(host);
@@ -257,7 +307,7 @@ const uint8_t* register_packed(Backend& b, const uint8_t* host, size_t bytes) {
   }
   void* d = nullptr;
   BM_HIP_CHECK_RET(hipMalloc(&d, bytes ? bytes : 1), nullptr);
-  BM_HIP_CHECK_RET(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, b.stream), nullptr);
+  BM_HIP_CHECK_RET(bm::upload(d, host, bytes, b.stream), nullptr);
   BM_HIP_CHECK_RET(bm::launch_canonicalize((uint8_t*)d, bytes, b.stream), nullptr);
   BM_HIP_CHECK_RET(hipStreamSynchronize(b.stream), nullptr);
   b.packed[host] = Registered{d, bytes};
@@ -272,8 +322,7 @@ const uint8_t* packed_for_call(Backend& b, const uint8_t* host, size_t bytes) {
   auto it = b.packed.find(host);
   if (it != b.packed.end() && it->second.bytes >= bytes) return (const uint8_t*)it->second.dev;
   if (!ensure_dev(b.d_w, bytes ? bytes : 1)) return nullptr;
-  BM_HIP_CHECK_RET(hipMemcpyAsync(b.d_w.ptr, host, bytes, hipMemcpyHostToDevice, b.stream),
-                   nullptr);
+  BM_HIP_CHECK_RET(bm::upload(b.d_w.ptr, host, bytes, b.stream), nullptr);
   BM_HIP_CHECK_RET(bm::launch_canonicalize((uint8_t*)b.d_w.ptr, bytes, b.stream), nullptr);
   BM_HIP_CHECK_RET(hipStreamSynchronize(b.stream), nullptr);
   return (const uint8_t*)b.d_w.ptr;
@@ -284,7 +333,8 @@ const float* floats_for_call(Backend& b, const float* host, size_t count) {
   auto it = b.floats.find(host);
   if (it != b.floats.end() && it->second.bytes >= bytes) return (const float*)it->second.dev;
   if (!ensure_dev(b.d_g, bytes ? bytes : 4)) return nullptr;
-  BM_HIP_CHECK_RET(hipMemcpy(b.d_g.ptr, host, bytes, hipMemcpyHostToDevice), nullptr);
+  BM_HIP_CHECK_RET(bm::upload(b.d_g.ptr, host, bytes, b.stream), nullptr);
+  BM_HIP_CHECK_RET(hipStreamSynchronize(b.stream), nullptr);
   return (const float*)b.d_g.ptr;
 }
 
@@ -298,7 +348,8 @@ const float* register_floats(Backend& b, const float* host, size_t count) {
   }
   void* d = nullptr;
   BM_HIP_CHECK_RET(hipMalloc(&d, bytes ? bytes : 4), nullptr);
-  BM_HIP_CHECK_RET(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice), nullptr);
+  BM_HIP_CHECK_RET(bm::upload(d, host, bytes, b.stream), nullptr);
+  BM_HIP_CHECK_RET(hipStreamSynchronize(b.stream), nullptr);
   b.floats[host] = Registered{d, bytes};
   return (const float*)d;
 }
@@ -421,14 +472,22 @@ extern "C" bool bm_hip_set_mmap(const void* base, size_t size) {
     // not a BIT2 image: tensors are uploaded lazily on first use
     return true;
   }
+  // what the table's entries read: the packed BitLinear weights and their
+  // norms (in_proj.norm, out_proj.norm, lm_head.norm) and norm_f; not the
+  // embedding (vocab x d_model floats the decode reads on the CPU) nor the
+  // SSM parameters
+  const int first_tail = 1 + BM_L_COUNT * v.n_layers;
   for (int i = 0; i < v.n_tensors; ++i) {
     const bm_bit2_tensor_t* t = &v.tensors[i];
+    const int which = (i - 1) % BM_L_COUNT;
+    const bool norm = i >= first_tail ||
+                      (i >= 1 && (which == BM_L_IN_NORM || which == BM_L_OUT_NORM));
     if (t->is_bitnet) {
       if (!register_packed(b, t->packed, (size_t)t->rows * (size_t)((t->cols + 3) / 4))) {
         bm_bit2_view_free(&v);
         return false;
       }
-    } else if (!register_floats(b, t->data, t->n_elements)) {
+    } else if (norm && !register_floats(b, t->data, t->n_elements)) {
       bm_bit2_view_free(&v);
       return false;
     }
