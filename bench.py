@@ -122,6 +122,11 @@ def leg_decode(L, steps, warmup, sampled=False, fast=False):
     L.bm_hip_synchronize()
     wall = time.perf_counter() - t0
     toks = np.concatenate([first, m.tokens(steps)])
+    # the step's kernels one at a time (layer 0, launched back to back on
+    # the model's stream between events): the roofline's live durations
+    ktimes = {name: round(m.time_kernel(which, 0, 200), 3) for name, which in
+              (("k_inproj_ssm", 0), ("out_proj", 1), ("lm_head", 2))}
+    m.reset()
     samp = None
     if sampled:
         # the same model and prompt with the device sampler
@@ -188,7 +193,7 @@ def leg_decode(L, steps, warmup, sampled=False, fast=False):
         ref = gold["tokens"]
         n = min(len(ref), len(toks))
         match = toks[:n].tolist() == ref[:n]
-    return wall, dev_ms, match, samp, prefill, fres
+    return wall, dev_ms, match, samp, prefill, fres, ktimes
 
 
 def leg_d255m(L, fast=False):
@@ -375,7 +380,7 @@ def gemv1_inputs():
             np.ones(K, np.float32), K, N, 0.02)
 
 
-def leg_gemv1(L, reps=200):
+def leg_gemv1(L, reps=200, cpu=True):
     packed, x, g, K, N, scale = gemv1_inputs()
     dW, dx, dg = (bh.DeviceBuffer.from_array(a) for a in (packed, x, g))
     dout, dq, ds = bh.DeviceBuffer(4 * N), bh.DeviceBuffer(K), bh.DeviceBuffer(4)
@@ -455,7 +460,17 @@ def leg_gemv1(L, reps=200):
                     "= the same entry on a model image registered by bm_hip_set_mmap "
                     "(K=1024 -> N=4192), per call: one kernel reading x from and writing its "
                     "results to mapped host memory, completion polled by the host")
-    res.update(cpu_gemv1())
+    res["roofline_cold"] = roofline_obj(
+        "k_rows_fused, K=1024 form (RMSNorm + int8 + GEMV, one launch)",
+        "bitlinear_k1024_n4384", "gemv1", wbytes, cold_us,
+        "config 1 (K=1024 -> N=4384, one token) through bm_hip_bitlinear_dev, weights cold "
+        "(460 copies used in turn); avg_us: HIP events over 460 back-to-back calls, launch "
+        "gaps included; bytes: packed weights")
+    res["roofline_warm"] = roofline_obj(
+        "k_rows_fused, K=1024 form", "bitlinear_k1024_n4384_warm", "gemv1", wbytes,
+        dev_us, "the same call with the weights cache-resident")
+    if cpu:
+        res.update(cpu_gemv1())
     return res
 
 
@@ -568,13 +583,29 @@ def leg_stress(L, reps=10):
             b.free()
     for c in cold:
         c.free()
-    out["note"] = ("int8 prep + product per call, canonical=0 (code 11 handled in-kernel); warm: "
+    out["note"] = ("M=1: one launch (k_rows_i8); M=16: k_prep_i8 + k_gemm_small; M=4096: "
+                   "k_prep_i8 + k_gemm; canonical=0 (code 11 handled in-kernel); warm: "
                    "the one 16.8 MB weight tensor stays cache-resident across calls; cold: 32 "
                    "copies (537 MB) used in turn, so each call streams its weights from HBM")
+    wb = N * K // 4
+    out["roofline_m1_cold"] = roofline_obj(
+        "k_rows_i8, K=8192 form (int8 GEMV, one launch)", "stress_m1", "stress",
+        wb + K + 4 * N, out["M1"]["cold_us"],
+        "bytes: packed weights + int8 input + int32 output; avg_us: HIP events over 64 "
+        "back-to-back calls on cold weights")
+    out["roofline_m16_cold"] = roofline_obj(
+        "k_prep_i8 + k_gemm_small (M=16)", "stress_m16", "stress",
+        wb + 16 * K + 4 * 16 * N, out["M16"]["cold_us"],
+        "bytes: packed weights + int8 inputs + int32 outputs; avg_us: both launches of a call, "
+        "HIP events over 64 calls on cold weights")
     return out
 
 
 def leg_roofline(L, reps=5):
+    """The GEMV's streaming ceiling (gemv_stream_ceiling): the 1B in_proj's
+    K=2048 row GEMV over 126 stacked copies of its rows (540 MB in one
+    launch), no BASELINE config -- the rate the row kernel reaches once
+    launch and latency costs vanish."""
     K, N_layer = 2048, 2 * 4096 + 3 * 64              # in_proj 2048 -> 8384
     row_bytes = K // 4
     target = 512 << 20
@@ -630,6 +661,51 @@ def decode_kernel_avg_us(name):
             except ValueError:
                 continue
     return None
+
+
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_per_launch.txt")
+PROFILE_FILES = {
+    "decode": os.path.join(ROOT, "profiles", "decode_1b_kernels.txt"),
+    "gemv1": os.path.join(ROOT, "profiles", "bitlinear_k1024_kernels.txt"),
+    "stress": os.path.join(ROOT, "profiles", "stress_k8192_kernels.txt"),
+}
+
+
+def traffic_of(key):
+    """HBM bytes per launch of a kernel/workload from the committed counter
+    summary (lines 'traffic <key> <read B> <written B>': FETCH_SIZE and
+    WRITE_SIZE per dispatch, calibrated with a copy of known size)."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            f = line.split()
+            if len(f) == 4 and f[0] == "traffic" and f[1] == key:
+                return int(f[2]) + int(f[3])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def profile_avg_us(which, name):
+    """Average duration (us) of a kernel in a committed rocprofv3 summary:
+    its line 'avg_us <name> <value>'."""
+    try:
+        for line in open(PROFILE_FILES[which]):
+            f = line.split()
+            if len(f) == 3 and f[0] == "avg_us" and f[1] == name:
+                return float(f[2])
+    except (OSError, ValueError, KeyError):
+        pass
+    return None
+
+
+def roofline_obj(kernel, key, which, bytes_per_launch, us, note):
+    """A roofline object for one kernel: algorithmic bytes per launch over
+    its live average duration, against the HBM peak."""
+    ach = bytes_per_launch / (us * 1e-6) / 1e9
+    return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                frac=round(ach / HBM_PEAK_GBPS, 4), traffic=traffic_of(key), kernel=kernel,
+                bytes_per_launch=bytes_per_launch, avg_us=round(us, 3),
+                profile_avg_us=profile_avg_us(which, key), note=note)
 
 
 def roofline_decode(c, dev_ms_per_step):
@@ -1151,7 +1227,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--legs",
-                    default="decode,sampled,fast,roofline,mfma,prefill,d255m,gemv1,stress,vendor,"
+                    default="decode,sampled,fast,ceiling,mfma,prefill,d255m,gemv1,stress,vendor,"
                             "dropin,cpu")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1187,8 +1263,11 @@ def main():
         sys.exit("bm_hip_init: " + bh.last_error())
     res = {}
     if "decode" in legs:
-        wall, dev_ms, match, samp, pf, fres = leg_decode(L, a.steps, a.warmup, "sampled" in legs,
-                                                         "fast" in legs)
+        wall, dev_ms, match, samp, pf, fres, ktimes = leg_decode(L, a.steps, a.warmup,
+                                                                 "sampled" in legs,
+                                                                 "fast" in legs)
+        res["kernel_us"] = ktimes
+        log("decode kernels, live: %s" % json.dumps(ktimes))
         res["fast"] = fres
         if fres:
             log("fast-mode decode: %s" % json.dumps(fres))
@@ -1199,9 +1278,9 @@ def main():
         log("decode: %d steps in %.2f ms wall (%.2f ms device)" % (a.steps, wall * 1e3, dev_ms))
         if samp:
             log("sampled decode: %s" % json.dumps(samp))
-    roof = leg_roofline(L) if "roofline" in legs else None
+    roof = leg_roofline(L) if "ceiling" in legs else None
     if roof:
-        log("roofline: %.1f GB/s (%.1f%% of HBM peak), %.1f us per launch"
+        log("GEMV stream ceiling: %.1f GB/s (%.1f%% of HBM peak), %.1f us per launch"
             % (roof["achieved"], 100 * roof["frac"], roof["launch_us"]))
     mf = leg_mfma(L) if "mfma" in legs else None
     if mf:
@@ -1218,7 +1297,7 @@ def main():
         log("fast-mode quantizer: %s" % json.dumps(fq))
     if d255:
         log("255M-shape decode: %s" % json.dumps(d255))
-    g1 = leg_gemv1(L) if "gemv1" in legs else None
+    g1 = leg_gemv1(L, cpu="cpu" in legs) if "gemv1" in legs else None
     if g1:
         log("K=1024 N=4384 BitLinear: %s" % json.dumps(g1))
     strs = leg_stress(L) if "stress" in legs else None
@@ -1270,14 +1349,37 @@ def main():
         if strs:
             strs["cpu"] = cpu_of("stress")
     if "decode" in res:
-        line["roofline_decode"] = roofline_decode(CFG_1B, line["device_ms_per_step"])
+        c = CFG_1B
+        dm, di, nh = c["d_model"], 2 * c["d_model"], c["n_heads"]
+        kt = res["kernel_us"]
+        line["roofline"] = roofline_obj(
+            "k_inproj_ssm (1B in_proj 2048->8384: RMSNorm + int8 + GEMV + the SSM step of its "
+            "heads, one launch per layer)", "k_inproj_ssm", "decode", (2 * di + 3 * nh) * dm // 4,
+            kt["k_inproj_ssm"],
+            "dominant kernel of the headline decode; bytes: the layer's packed in_proj weights; "
+            "avg_us: 200 launches back to back on the model's stream between HIP events "
+            "(bm_hip_model_time_kernel, layer 0)")
+        rd = roofline_decode(c, line["device_ms_per_step"])
+        rd["kernels"] = {
+            "k_inproj_ssm": line["roofline"],
+            "out_proj": roofline_obj(
+                "k_rows_fused, out_proj form (1B out_proj 4096->2048: RMSNorm + int8 + GEMV + "
+                "residual)",
+                "out_proj", "decode", di * dm // 4, kt["out_proj"], "layer 0, live"),
+            "lm_head": roofline_obj(
+                "k_rows_fused, LM head form (final norm + LM head 2048->50257 + greedy "
+                "candidates)", "lm_head", "decode", c["vocab"] * dm // 4, kt["lm_head"],
+                "live"),
+        }
+        line["roofline_decode"] = rd
     line["decode_sampled"] = res.get("sampled")
     if res.get("fast") or fq:
         line["decode_fast"] = dict(res.get("fast") or {}, quantizer=fq,
                                    note="opt-in fast mode: sums of squares as a pairwise tree, "
                                         "not the reference's bits; value stays parity mode")
     line["prefill_1b"] = res.get("prefill_model")
-    line["roofline"] = roof
+    line.setdefault("roofline", None)
+    line["gemv_stream_ceiling"] = roof
     line["mfma_ceiling"] = mf
     line["prefill_gemm"] = pre
     line["decode_255m"] = d255

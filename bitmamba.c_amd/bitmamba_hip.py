@@ -94,6 +94,7 @@ SIGNATURES = {
     "bm_hip_model_step": (_i, [_vp, _i, _vp, _i, _f]),
     "bm_hip_model_set_sampler": (_i, [_vp, _f, _f, _f, _i]),
     "bm_hip_model_set_fast": (_i, [_vp, _i]),
+    "bm_hip_model_time_kernel": (_i, [_vp, _i, _i, _i, _vp]),
     "bm_hip_model_seed": (_i, [_vp, _u64]),
     "bm_hip_sample_workspace_bytes": (_sz, [_i]),
     "bm_hip_sample_advanced": (_i, [_vp, _i, _f, _f, _f, _i, _vp, _vp, _vp, _vp]),
@@ -307,6 +308,14 @@ class Model:
 
     def set_fast(self, on):
         check(lib().bm_hip_model_set_fast(self.h, int(bool(on))), "set_fast")
+
+    def time_kernel(self, which, layer=0, reps=50):
+        """Average microseconds per launch of one decode kernel (0 in_proj +
+        SSM, 1 out_proj, 2 LM head); changes the state: reset afterwards."""
+        us = C.c_float(0.0)
+        check(lib().bm_hip_model_time_kernel(self.h, which, layer, reps, C.byref(us)),
+              "time_kernel")
+        return float(us.value)
 
     def prefill(self, tokens):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)

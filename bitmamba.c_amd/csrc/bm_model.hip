@@ -937,6 +937,54 @@ extern "C" int bm_hip_model_set_fast(bm_hip_model_t* m, int on) {
   return 0;
 }
 
+// One kernel of the decode step launched `reps` times back to back on the
+// model's stream, timed with events on that stream: which 0 = layer's
+// in_proj + SSM step, 1 = layer's out_proj (+ residual), 2 = the LM head
+// (greedy candidates).  Changes the recurrent state and the activations.
+extern "C" int bm_hip_model_time_kernel(bm_hip_model_t* m, int which, int layer, int reps,
+                                        float* avg_us) {
+  if (!m || !avg_us || reps < 1 || which < 0 || which > 2 || layer < 0 || layer >= m->nl) {
+    bm_set_error("bm_hip_model_time_kernel: bad arguments");
+    return -1;
+  }
+  const int dm = m->dm, di = m->di;
+  if (!bm::inproj_ssm_fits(dm, m->hd) || !bm::rows_fit(di) || !bm::rows_fit(dm)) {
+    bm_set_error("bm_hip_model_time_kernel: the model's widths take the generic kernels");
+    return -1;
+  }
+  const Layer& Ly = m->L[layer];
+  float* cs = m->conv_state + (size_t)layer * 3 * di;
+  float* ss = m->ssm_state + (size_t)layer * di;
+  hipStream_t s = m->stream;
+  auto launch = [&]() -> hipError_t {
+    if (which == 0)
+      return bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
+                                   Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
+                                   m->ctl, s, m->fast);
+    if (which == 1)
+      return bm::launch_outproj(m->y, di, Ly.out_norm, Ly.out_proj, dm, Ly.out_scale, m->x, s,
+                                m->fast);
+    return bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab, m->lm_scale,
+                              m->logits, 1, m->temp, m->part_v, m->part_i, s, m->fast);
+  };
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  MCHECK(hipEventCreate(&e0));
+  MCHECK(hipEventCreate(&e1));
+  hipError_t e = launch();
+  if (e == hipSuccess) e = launch();  // warm
+  if (e == hipSuccess) e = hipEventRecord(e0, s);
+  for (int i = 0; i < reps && e == hipSuccess; ++i) e = launch();
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  MCHECK(e);
+  *avg_us = ms * 1000.0f / (float)reps;
+  return 0;
+}
+
 extern "C" int bm_hip_model_seed(bm_hip_model_t* m, uint64_t seed) {
   const uint64_t s = seed ? seed : 0x853c49e6748fea9bULL;  // rng_seed (src/utils.c:121-124)
   MCHECK(hipMemcpyAsync(m->rng, &s, sizeof(s), hipMemcpyHostToDevice, m->stream));

@@ -314,6 +314,16 @@ int bm_hip_model_step(bm_hip_model_t *m,
  * chains.  Results then differ from the reference in the last bits of
  * 1/rms and occasionally by one int8 step.  0. */
 int bm_hip_model_set_fast(bm_hip_model_t *m, int on);
+/* Measurement (no counterpart in the reference; for benchmarks and
+ * profiles): one kernel of the decode step, launched reps times back to
+ * back on the model's stream after two untimed launches, timed with events
+ * on that stream.  which: 0 = in_proj + SSM step of `layer`, 1 = out_proj
+ * (+ residual) of `layer`, 2 = the LM head (greedy candidates).  Writes the
+ * average microseconds per launch to *avg_us.  The recurrent state and the
+ * activations change: reset the model (or load a saved state) afterwards.
+ * 0, or -1 (bm_hip_last_error) for bad arguments or widths that take the
+ * generic kernels. */
+int bm_hip_model_time_kernel(bm_hip_model_t *m, int which, int layer, int reps, float *avg_us);
 /* Sampling parameters of every later step, generate and decode: the
  * temp, min_p, top_p, top_k arguments of model_forward_step
  * (src/model.c:1175-1183), sampled on the device by sample_advanced
