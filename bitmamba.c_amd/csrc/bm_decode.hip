@@ -23,8 +23,16 @@
 
 namespace bm {
 
-// control words shared with bm_model.hip
-enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3 };
+// control words shared with bm_model.hip.  CTL_DONE: 0 steps always run,
+// 1 armed (generate with stop_on_eos), 2 the end token was picked: every
+// later step leaves the state, the activations, the logits and the
+// bookkeeping untouched, so the state stops where the reference's loop
+// stops (src/main.c:473-500)
+// (CTL_DONE beside CTL_POS: k_inproj_ssm reads both with one 8-byte load)
+enum { CTL_POS = 0, CTL_DONE = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_TOKEN = 4 };
+constexpr int kDoneArmed = 1, kDoneStopped = 2;
+
+__device__ __forceinline__ bool is_end_token(int t) { return t == 50256 || t == 0; }
 constexpr int kHist = 256;
 
 __device__ __forceinline__ float silu_r(float x) {
@@ -526,7 +534,8 @@ __device__ __forceinline__ void lane_sums(const uint32_t (&xa)[P][16], int (&xs)
 struct DropOut {
   float* xn;        // normalized input, written by block 0 (or null)
   int8_t* xq;       // int8 input, written by block 0 (or null)
-  unsigned* flags;  // DROP: host-mapped completion words, one per block
+  unsigned* flags;  // DROP: host-mapped completion words, one per block;
+                    // LM head: the step's CTL_DONE word (or null)
   unsigned seq;
   float* scale;     // scale_x, written by block 0 (or null)
 };
@@ -562,6 +571,14 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
     stage_load<C>(sg, PRENORM ? gamma_pre : gamma, K);
     if constexpr (PRENORM) stage_load<C>(sg2, gamma, K);
   }
+  // the LM head of a stopped decode (CTL_DONE, passed in dr.flags, which
+  // only the DROP form uses otherwise) stores nothing (the word is a scalar
+  // load the wave waits for: ~0.1 us, once per token); the out_proj of such
+  // a step needs no test, its input y is zero (k_inproj_ssm).  DropOut keeps
+  // its size: one more pointer in it (376 -> 384 bytes of kernel arguments)
+  // made every out_proj launch 0.19 us slower
+  bool stopped = false;
+  if constexpr (PRENORM) stopped = dr.flags && *(const int*)dr.flags == kDoneStopped;
 
   uint4 wv[NPF][P];
   auto load_rows = [&]() {
@@ -636,7 +653,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   // area, free after the prologue; a block owns at most 4 * NPF * RPW rows)
   const int r0 = g0 * RPW;
   auto emit = [&](int r, float o, float res) {
-    if (u == 0 && r < N) {
+    if (u == 0 && r < N && !stopped) {
       if (PICK == 2) o = __fmul_rn(o, inv_temp);
       if (DROP)
         l.sq[r - r0] = o;
@@ -704,7 +721,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
     }
     if (lane == 0) l.bc[16 + wave] = best_v;
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0 && !stopped) {
       for (int k = 1; k < 4; ++k)
         if (l.bc[16 + k] > best_v) best_v = l.bc[16 + k];
       part_v[blockIdx.x] = best_v;
@@ -724,7 +741,7 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
       ((int*)l.bc)[20 + wave] = best_i;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0 && !stopped) {
       for (int k = 1; k < 4; ++k) {
         const float v = l.bc[16 + k];
         const int i = ((int*)l.bc)[20 + k];
@@ -908,7 +925,7 @@ struct SsmArgs {
   int hd, di;
 };
 
-template <int T, int P, int NPF, int C, bool WP>
+template <int T, int P, int NPF, int C, bool WP, bool GATED>
 __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma,
                                                     const uint8_t* __restrict__ W, float w_scale,
@@ -933,7 +950,15 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
 
   // the ring position first (nothing waits for it until the SSM step), the
   // input vector next (the prologue waits for it), then the weights
-  const int pos = a.ctl[CTL_POS];
+  int pos;
+  bool stopped = false;  // GATED: a stopped decode leaves the state as it is
+  if constexpr (GATED) {
+    const int2 pos_done = *(const int2*)a.ctl;  // CTL_POS, CTL_DONE
+    pos = pos_done.x;
+    stopped = pos_done.y == kDoneStopped;
+  } else {
+    pos = a.ctl[CTL_POS];
+  }
   float4 sx[WP ? 1 : C], sg[WP ? 1 : C];
   SplitIn<C, false> sin;
   if constexpr (WP) {
@@ -1015,7 +1040,7 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
     conv = __fadd_rn(conv, __fmul_rn(tap1, cw1));
     conv = __fadd_rn(conv, __fmul_rn(tap2, cw2));
     conv = __fadd_rn(conv, __fmul_rn(xin, cw3));
-    a.cs[(size_t)pos * a.di + idx] = xin;  // the oldest tap is overwritten
+    if (!stopped) a.cs[(size_t)pos * a.di + idx] = xin;  // the oldest tap is overwritten
     s_tail[c] = silu_r(conv);
   } else if (wave == 1 && lane < kCB) {
     s_tail[kCB + lane] = silu_r(s_proj[lane]);
@@ -1025,7 +1050,11 @@ __global__ __launch_bounds__(256) void k_inproj_ssm(const float* __restrict__ x,
     s_tail[2 * kCB + 1] = libm::expf_glibc(__fmul_rn(Ah, dt_val));
   }
   __syncthreads();
-  if (tid < kCB) {
+  if (tid < kCB && stopped) {
+    // a stopped step: the state stays, and y = 0 makes the out_proj that
+    // follows add exactly +0 to x (RMSNorm of zeros, int8 zeros, zero totals)
+    a.y[idx] = 0.0f;
+  } else if (tid < kCB) {
     const float dt_val = s_tail[2 * kCB], decay = s_tail[2 * kCB + 1];
     const float Bdt = __fmul_rn(s_proj[2 * kCB], dt_val);
     const float C_val = s_proj[2 * kCB + 1];
@@ -1050,6 +1079,10 @@ __global__ void k_ssm_heads(const float* __restrict__ proj, int hd, int di,
   if (c >= hd) return;
   const float* __restrict__ ph = proj + (size_t)h * (2 * hd + 3);
   const int idx = h * hd + c;
+  if (ctl[CTL_DONE] == kDoneStopped) {  // a stopped decode keeps its state; y = 0 (see
+    y[idx] = 0.0f;                       // k_inproj_ssm)
+    return;
+  }
   const int pos = ctl[CTL_POS];
   const int t1 = pos + 1 < 3 ? pos + 1 : pos - 2;
   const int t2 = pos + 2 < 3 ? pos + 2 : pos - 1;
@@ -1090,6 +1123,7 @@ __global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
   const int step = tid == 0 ? ctl[CTL_STEP] : 0;
   const int hcount = tid == 0 ? ctl[CTL_HCOUNT] : 0;
   const int pos = tid == 0 ? ctl[CTL_POS] : 0;
+  const int done = tid == 0 ? ctl[CTL_DONE] : 0;
   float bv = -1e9f;
   int bi = 0x7fffffff;
   for (int b = tid; b < n_parts; b += blockDim.x) {
@@ -1121,16 +1155,20 @@ __global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
         bi = si[k];
       }
     const int best = bi == 0x7fffffff ? 0 : bi;
-    if (out_tokens) out_tokens[step] = best;
-    ctl[CTL_STEP] = step + 1;
-    ctl[CTL_TOKEN] = best;
-    hist[hcount % kHist] = best;
-    ctl[CTL_HCOUNT] = hcount + 1;
-    ctl[CTL_POS] = pos + 1 < 3 ? pos + 1 : 0;  // src/block.c:107
-    s_tok = best;
+    if (done != kDoneStopped) {  // a stopped decode changes nothing
+      if (out_tokens) out_tokens[step] = best;
+      ctl[CTL_STEP] = step + 1;
+      ctl[CTL_TOKEN] = best;
+      hist[hcount % kHist] = best;
+      ctl[CTL_HCOUNT] = hcount + 1;
+      ctl[CTL_POS] = pos + 1 < 3 ? pos + 1 : 0;  // src/block.c:107
+      if (done == kDoneArmed && is_end_token(best)) ctl[CTL_DONE] = kDoneStopped;
+    }
+    s_tok = done == kDoneStopped ? -1 : best;
   }
   __syncthreads();
   const int tok = s_tok;
+  if (tok < 0) return;
   const float* __restrict__ row = embed + (size_t)tok * dm;
   if (dm % 4 == 0 && dm <= 4 * 4 * 256) {
     // every load of the row in flight before the first store (16-byte
@@ -1263,37 +1301,48 @@ hipError_t launch_rows_i8(const int8_t* xq, int M, int ldx, int K, const uint8_t
 }
 
 // in_proj + SSM for every head: y (and the states) updated in one launch
+template <bool GATED>
+static hipError_t inproj_ssm_t(const float* x, int K, const float* gamma, const uint8_t* W,
+                               float w_scale, const SsmArgs& args, const dim3& grid,
+                               size_t lds, hipStream_t s, bool fast) {
+  const dim3 block(256);
+  if (K == 1024)
+    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, true, GATED>), grid, block, lds, s, x, K, gamma,
+                       W, w_scale, args, (int)fast);
+  else if (K == 2048)
+    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, true, GATED>), grid, block, lds, s, x, K, gamma,
+                       W, w_scale, args, (int)fast);
+  else if (K == 4096)
+    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, true, GATED>), grid, block, lds, s, x, K, gamma,
+                       W, w_scale, args, (int)fast);
+  else if (K <= 1024)
+    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, false, GATED>), grid, block, lds, s, x, K,
+                       gamma, W, w_scale, args, (int)fast);
+  else if (K <= 2048)
+    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, false, GATED>), grid, block, lds, s, x, K,
+                       gamma, W, w_scale, args, (int)fast);
+  else if (K <= 4096)
+    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, false, GATED>), grid, block, lds, s, x, K,
+                       gamma, W, w_scale, args, (int)fast);
+  else
+    hipLaunchKernelGGL((k_inproj_ssm<64, 2, 9, 8, false, GATED>), grid, block, lds, s, x, K,
+                       gamma, W, w_scale, args, (int)fast);
+  return hipGetLastError();
+}
+
+// gated: the kernel reads the done word (CTL_DONE) and, once stopped, leaves
+// the state as it is (the step graph of a generate with stop_on_eos)
 hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const uint8_t* W,
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
                              const float* cw, const float* cb, float* cs, float* ssm,
                              const float* D, float* y, const int* ctl, hipStream_t s,
-                             bool fast) {
+                             bool fast, bool gated) {
   if (!inproj_ssm_fits(K, hd)) return hipErrorInvalidValue;
   const SsmArgs args{dt_bias, A, cw, cb, cs, ssm, D, y, ctl, hd, nh * hd};
-  const dim3 grid(nh * (hd / kCB)), block(256);
+  const dim3 grid(nh * (hd / kCB));
   const size_t lds = lds_bytes(K);
-  if (K == 1024)
-    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, true>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  else if (K == 2048)
-    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, true>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  else if (K == 4096)
-    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, true>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  else if (K <= 1024)
-    hipLaunchKernelGGL((k_inproj_ssm<16, 1, 3, 1, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  else if (K <= 2048)
-    hipLaunchKernelGGL((k_inproj_ssm<32, 1, 5, 2, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  else if (K <= 4096)
-    hipLaunchKernelGGL((k_inproj_ssm<64, 1, 9, 4, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  else
-    hipLaunchKernelGGL((k_inproj_ssm<64, 2, 9, 8, false>), grid, block, lds, s, x, K, gamma, W,
-                       w_scale, args, (int)fast);
-  return hipGetLastError();
+  return gated ? inproj_ssm_t<true>(x, K, gamma, W, w_scale, args, grid, lds, s, fast)
+               : inproj_ssm_t<false>(x, K, gamma, W, w_scale, args, grid, lds, s, fast);
 }
 
 hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
@@ -1315,15 +1364,18 @@ int lm_head_blocks(int N, int K) { return rows_blocks<kLmNpf>(N, K); }
 // part_i), 2 logits times 1/temp with the blocks' maxima (part_v)
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
                           const uint8_t* W, int N, float w_scale, float* logits, int pick,
-                          float temp, float* part_v, int* part_i, hipStream_t s, bool fast) {
+                          float temp, float* part_v, int* part_i, hipStream_t s, bool fast,
+                          const int* gate) {
+  DropOut dr{};
+  dr.flags = (unsigned*)gate;
   if (pick == 1)
     return rows_t<kLmNpf, true, 0, 1>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, part_i,
-                                      s, 1.0f, DropOut{}, fast);
+                                      s, 1.0f, dr, fast);
   if (pick == 2)
     return rows_t<kLmNpf, true, 0, 2>(x, K, norm_f, lm_norm, W, N, w_scale, logits, part_v, nullptr,
-                                      s, temp, DropOut{}, fast);
+                                      s, temp, dr, fast);
   return rows_t<kLmNpf, true, 0, 0>(x, K, norm_f, lm_norm, W, N, w_scale, logits, nullptr, nullptr,
-                                    s, 1.0f, DropOut{}, fast);
+                                    s, 1.0f, dr, fast);
 }
 
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,

@@ -27,7 +27,10 @@
 namespace bm {
 
 // control block in device memory
-enum { CTL_POS = 0, CTL_TOKEN = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_WORDS = 8 };
+// CTL_DONE: 0 steps always run, 1 armed (generate with stop_on_eos), 2 the
+// end token was picked: later steps change nothing (bm_decode.hip)
+enum { CTL_POS = 0, CTL_DONE = 1, CTL_STEP = 2, CTL_HCOUNT = 3, CTL_TOKEN = 4, CTL_WORDS = 8 };
+constexpr int kDoneArmed = 1, kDoneStopped = 2;
 constexpr int kHistory = 256;  // HISTORY_MAX (src/main.c:19)
 
 __device__ __forceinline__ float silu_ref(float x) {
@@ -261,9 +264,13 @@ __global__ void k_advance_pos(int* ctl, int n) {
   if (threadIdx.x == 0 && blockIdx.x == 0) ctl[CTL_POS] = (ctl[CTL_POS] + n) % 3;
 }
 
-// a decode run's steps count from 0 (the tokens buffer is filled from its start)
+// a decode run's steps count from 0 (the tokens buffer is filled from its
+// start) and always run (a continuation after an end token goes on from it)
 __global__ void k_restart_steps(int* ctl) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) ctl[CTL_STEP] = 0;
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    ctl[CTL_STEP] = 0;
+    ctl[CTL_DONE] = 0;
+  }
 }
 
 // x[t] = embed[tok[t]]; out-of-range ids read row 0 (src/model.c:1116-1122)
@@ -287,6 +294,7 @@ __global__ void k_neg_exp(const float* __restrict__ a, float* __restrict__ out, 
 // entries can be processed in parallel.
 __global__ void k_penalty(float* __restrict__ logits, int vocab, const int* __restrict__ hist,
                           const int* __restrict__ ctl, float penalty) {
+  if (ctl[CTL_DONE] == kDoneStopped) return;  // the logits stay those of the end token's step
   const int count = ctl[CTL_HCOUNT];
   const int len = count < kHistory ? count : kHistory;
   const int j = threadIdx.x;
@@ -341,6 +349,7 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ 
         bi = si[w];
       }
     const int best = bi == 0x7fffffff ? 0 : bi;
+    if (ctl[CTL_DONE] == kDoneStopped) return;  // a stopped decode changes nothing
     const int step = ctl[CTL_STEP];
     if (out_tokens) out_tokens[step] = best;
     ctl[CTL_STEP] = step + 1;
@@ -348,6 +357,7 @@ __global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ 
     hist[ctl[CTL_HCOUNT] % kHistory] = best;
     ctl[CTL_HCOUNT] += 1;
     ctl[CTL_POS] = ctl[CTL_POS] + 1 < 3 ? ctl[CTL_POS] + 1 : 0;  // src/block.c:107
+    if (ctl[CTL_DONE] == kDoneArmed && (best == 50256 || best == 0)) ctl[CTL_DONE] = kDoneStopped;
   }
 }
 
@@ -360,21 +370,22 @@ hipError_t launch_inproj_ssm(const float* x, int K, const float* gamma, const ui
                              float w_scale, int nh, int hd, const float* dt_bias, const float* A,
                              const float* cw, const float* cb, float* cs, float* ssm,
                              const float* D, float* y, const int* ctl, hipStream_t s,
-                             bool fast);
+                             bool fast, bool gated = false);
 hipError_t launch_ssm_heads(const float* proj, int nh, int hd, const float* dt_bias,
                             const float* A, const float* cw, const float* cb, float* cs,
                             float* ssm, const float* D, float* y, const int* ctl, hipStream_t s);
 int lm_head_blocks(int N, int K);
 hipError_t launch_lm_head(const float* x, int K, const float* norm_f, const float* lm_norm,
                           const uint8_t* W, int N, float w_scale, float* logits, int pick,
-                          float temp, float* part_v, int* part_i, hipStream_t s, bool fast);
+                          float temp, float* part_v, int* part_i, hipStream_t s, bool fast,
+                          const int* gate = nullptr);
 hipError_t launch_pick(const float* part_v, const int* part_i, int n_parts, int* ctl, int* hist,
                        int* out_tokens, const float* embed, int dm, float* x, hipStream_t s);
 size_t sample_scratch_bytes(int V);
 hipError_t launch_sample(float* logits, int V, float temp, float min_p, float top_p, int top_k,
                          uint64_t* rng_state, void* scratch, const float* pmax, int npart,
                          int* ctl, int* hist, int* out_tokens, const float* embed, int dm,
-                         float* x, hipStream_t s);
+                         float* x, hipStream_t s, bool gated = false);
 
 }  // namespace bm
 
@@ -437,6 +448,9 @@ struct bm_hip_model {
   bool no_graph = false;
   // fast mode (bm_hip_model_set_fast): sums of squares as a pairwise tree
   bool fast = false, graph_fast = false;
+  // the step graph of a generate with stop_on_eos: its kernels read the
+  // done word (CTL_DONE) and change nothing once the end token is picked
+  bool gated = false, graph_gated = false;
 };
 
 namespace {
@@ -484,7 +498,7 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
     if (bm::inproj_ssm_fits(dm, m->hd)) {
       MCHECK(bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
                                    Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,
-                                   m->ctl, s, m->fast));
+                                   m->ctl, s, m->fast, m->gated));
     } else {
       if (rows_dm) {
         MCHECK(bm::launch_inproj(m->x, dm, Ly.in_norm, Ly.in_proj, m->pd, Ly.in_scale, m->proj,
@@ -512,7 +526,8 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
   if (rows_dm) {
     MCHECK(bm::launch_lm_head(m->x, dm, m->norm_f, m->lm_norm, m->lm_head, m->vocab,
                               m->lm_scale, m->logits, fused_pick ? 1 : (fused_scale ? 2 : 0),
-                              m->temp, m->part_v, m->part_i, s, m->fast));
+                              m->temp, m->part_v, m->part_i, s, m->fast,
+                              m->gated ? m->ctl + bm::CTL_DONE : nullptr));
   } else {
     // rms_norm(norm_f), then BitLinear with lm_head.norm (src/model.c:1225, 1259-1261)
     MCHECK(bm::launch_rms_norm(m->x, dm, m->norm_f, m->feat, m->scale + 8, s));
@@ -530,7 +545,7 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
     MCHECK(bm::launch_sample(m->logits, m->vocab, m->temp, m->min_p, m->top_p, m->top_k, m->rng,
                              m->samp_scratch, fused_scale ? m->part_v : nullptr,
                              fused_scale ? m->lm_blocks : 0, m->ctl, m->hist, out, m->embed, dm,
-                             m->x, s));
+                             m->x, s, m->gated));
   } else if (fused_pick) {
     MCHECK(bm::launch_pick(m->part_v, m->part_i, m->lm_blocks, m->ctl, m->hist, out, m->embed, dm,
                            m->x, s));
@@ -556,7 +571,8 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
   }
   const float samp[4] = {m->temp, m->min_p, m->top_p, (float)m->top_k};
   if (m->exec && m->graph_penalty == penalty && m->graph_with_out == write_out &&
-      m->graph_fast == m->fast && memcmp(samp, m->graph_samp, sizeof(samp)) == 0)
+      m->graph_fast == m->fast && m->graph_gated == m->gated &&
+      memcmp(samp, m->graph_samp, sizeof(samp)) == 0)
     return 0;
   if (m->exec) {
     (void)hipGraphExecDestroy(m->exec);
@@ -580,6 +596,7 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
   m->graph_penalty = penalty;
   m->graph_with_out = write_out;
   m->graph_fast = m->fast;
+  m->graph_gated = m->gated;
   memcpy(m->graph_samp, samp, sizeof(samp));
   return 0;
 }
@@ -774,7 +791,7 @@ int load_into(bm_hip_model* m, const bm_bit2_view_t& v) {
   return 0;
 }
 
-int set_ctl(bm_hip_model* m, int token, const int* history, int history_len) {
+int set_ctl(bm_hip_model* m, int token, const int* history, int history_len, int done = 0) {
   int h[bm::kHistory];
   const int len = history_len < bm::kHistory ? history_len : bm::kHistory;
   for (int j = 0; j < len; ++j) h[j] = history[history_len - len + j];
@@ -784,6 +801,7 @@ int set_ctl(bm_hip_model* m, int token, const int* history, int history_len) {
   ctl[bm::CTL_TOKEN] = token;
   ctl[bm::CTL_STEP] = 0;
   ctl[bm::CTL_HCOUNT] = len;
+  ctl[bm::CTL_DONE] = done;
   MCHECK(hipMemcpyAsync(m->ctl, ctl, sizeof(ctl), hipMemcpyHostToDevice, m->stream));
   if (len) MCHECK(hipMemcpyAsync(m->hist, h, (size_t)len * 4, hipMemcpyHostToDevice, m->stream));
   hipLaunchKernelGGL(bm::k_embed, dim3((m->dm + 255) / 256, 1), dim3(256), 0, m->stream,
@@ -915,6 +933,7 @@ extern "C" int bm_hip_model_prefill(bm_hip_model_t* m, const int32_t* tokens, in
 extern "C" int bm_hip_model_step(bm_hip_model_t* m, int token, const int* history,
                                  int history_len, float penalty) {
   if (token < 0 || token >= m->vocab) return 0;  // src/model.c:1188-1193
+  m->gated = false;
   if (set_ctl(m, token, history, history_len)) return -1;
   if (enqueue_step(m, m->stream, penalty, false)) return -1;
   int ctl[bm::CTL_WORDS];
@@ -1130,7 +1149,14 @@ extern "C" int bm_hip_model_generate(bm_hip_model_t* m, const int32_t* prompt, i
   // src/main.c:451-500: prefill all but the last prompt token, history =
   // the prompt, then greedy steps from the last prompt token
   if (n_prompt > 1 && bm_hip_model_prefill(m, prompt, n_prompt - 1)) return -1;
-  if (set_ctl(m, prompt[n_prompt - 1], prompt, n_prompt)) return -1;
+  // stop_on_eos: the step that picks the end token is the last that changes
+  // anything (src/main.c:498-500), for widths whose every step kernel reads
+  // the done word (the fused row kernels); other widths run all n_steps
+  const bool fused = bm::inproj_ssm_fits(m->dm, m->hd) && bm::rows_fit(m->di) &&
+                     bm::rows_fit(m->dm);
+  m->gated = stop_on_eos && fused;
+  if (set_ctl(m, prompt[n_prompt - 1], prompt, n_prompt, m->gated ? bm::kDoneArmed : 0))
+    return -1;
   if (ensure_out(m, n_steps > 0 ? n_steps : 1)) return -1;
   if (ensure_graph(m, penalty, true)) return -1;
   if (run_steps(m, n_steps, decode_ms)) return -1;
@@ -1148,6 +1174,7 @@ extern "C" int bm_hip_model_generate(bm_hip_model_t* m, const int32_t* prompt, i
 extern "C" int bm_hip_model_decode(bm_hip_model_t* m, int n_steps, float penalty,
                                    double* decode_ms) {
   // continues from the current device state (token, history, position)
+  m->gated = false;
   if (ensure_out(m, n_steps > 0 ? n_steps : 1)) return -1;
   if (ensure_graph(m, penalty, true)) return -1;
   // on the device, in stream order: no host copy of the control words

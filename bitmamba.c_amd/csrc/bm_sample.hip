@@ -45,7 +45,15 @@ constexpr int kThreads = 1024;
 constexpr int kBuckets = 128;      // HIST_BUCKETS (src/model.c:131)
 constexpr int kPartial = 256;      // PARTIAL_K (src/model.c:319)
 constexpr int kStage = 4096;       // candidates staged in LDS per serial pass
-constexpr int kCtlPos = 0, kCtlToken = 1, kCtlStep = 2, kCtlHcount = 3;
+constexpr int kCtlPos = 0, kCtlDone = 1, kCtlStep = 2, kCtlHcount = 3, kCtlToken = 4;
+constexpr int kDoneArmed = 1, kDoneStopped = 2;  // the done word (bm_decode.hip)
+
+// a decode stopped at its end token: the front kernels (given the done
+// word only in a gated step graph) return at once; k_sample and
+// k_sample_greedy skip their stores at the end
+__device__ __forceinline__ bool step_stopped(const int* ctl) {
+  return ctl && __builtin_amdgcn_readfirstlane(ctl[kCtlDone]) == kDoneStopped;
+}
 constexpr int kHist = 256;
 constexpr int kFront = 64;          // blocks of the O(V) passes (one wave of partials)
 constexpr int kFrontThreads = 256;
@@ -530,7 +538,7 @@ __device__ double ordered_sum(const Cand* __restrict__ c, int n, Smem& sm) {
 // in the step writes them) so that the bookkeeping at its end waits for no
 // load
 struct CtlSnap {
-  int step = 0, hcount = 0, pos = 0;
+  int step = 0, hcount = 0, pos = 0, done = 0;
 };
 __device__ __forceinline__ CtlSnap ctl_snap(const StepIO& io) {
   CtlSnap c;
@@ -538,6 +546,7 @@ __device__ __forceinline__ CtlSnap ctl_snap(const StepIO& io) {
     c.step = io.ctl[kCtlStep];
     c.hcount = io.ctl[kCtlHcount];
     c.pos = io.ctl[kCtlPos];
+    c.done = io.ctl[kCtlDone];
   }
   return c;
 }
@@ -556,6 +565,7 @@ __device__ void finish_step(int token, uint64_t rng, uint64_t* rng_state, const 
   io.hist[c.hcount % kHist] = token;
   ctl[kCtlHcount] = c.hcount + 1;
   ctl[kCtlPos] = c.pos + 1 < 3 ? c.pos + 1 : 0;  // src/block.c:107
+  if (c.done == kDoneArmed && (token == 50256 || token == 0)) ctl[kCtlDone] = kDoneStopped;
 }
 
 // the next token's embedding row (src/model.c:1116-1122), whole block
@@ -572,8 +582,10 @@ __device__ void embed_next(int token, const StepIO& io) {
 // also clears the histogram and the block counter of pass 2.  (The LM head
 // can do this pass itself, with its own blocks' maxima.)
 __global__ __launch_bounds__(kFrontThreads) void k_samp_scale(float* __restrict__ logits, int V,
-                                                              float temp, void* scratch) {
+                                                              float temp, void* scratch,
+                                                              const int* ctl) {
   __shared__ float red[kFrontThreads / 64];
+  if (step_stopped(ctl)) return;
   const Scratch sc = scratch_of(scratch, V);
   const int seg = front_seg(V);
   const int i0 = min(V, (int)blockIdx.x * seg), i1 = min(V, i0 + seg);
@@ -619,10 +631,11 @@ __global__ __launch_bounds__(kFrontThreads) void k_samp_hist(const float* __rest
                                                              int V, SampleParams p,
                                                              void* scratch,
                                                              const float* __restrict__ pmax,
-                                                             int npart) {
+                                                             int npart, const int* ctl) {
   constexpr int NW = kFrontThreads / 64;
   __shared__ int bhist[kBuckets];
   __shared__ int wcnt[NW];
+  if (step_stopped(ctl)) return;
   const Scratch sc = scratch_of(scratch, V);
   const int seg = front_seg(V);
   const int i0 = min(V, (int)blockIdx.x * seg), i1 = min(V, i0 + seg);
@@ -842,11 +855,16 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
 
   // the token to every thread, the step, the next embedding; leave the
   // histogram cleared for the next call
-  if (threadIdx.x == 0) sm.iwork[4] = token;
+  if (threadIdx.x == 0) {
+    sm.iwork[4] = token;
+    sm.iwork[5] = cs.done == kDoneStopped;
+  }
   __syncthreads();
   token = sm.iwork[4];
-  if (threadIdx.x == 0) finish_step(token, rng, rng_state, io, cs);
-  embed_next(token, io);
+  if (!sm.iwork[5]) {  // a stopped decode changes nothing
+    if (threadIdx.x == 0) finish_step(token, rng, rng_state, io, cs);
+    embed_next(token, io);
+  }
   if (threadIdx.x < kBuckets) sc.hist[threadIdx.x] = 0;
 }
 
@@ -857,6 +875,9 @@ __global__ __launch_bounds__(1024) void k_sample_greedy(const float* __restrict_
   __shared__ Smem sm;
   const CtlSnap cs = ctl_snap(io);
   const int token = argmax_scan(logits, V, -1e9f, sm);
+  if (threadIdx.x == 0) sm.iwork[5] = cs.done == kDoneStopped;
+  __syncthreads();
+  if (sm.iwork[5]) return;  // a stopped decode changes nothing
   if (threadIdx.x == 0) finish_step(token, *rng_state, rng_state, io, cs);
   embed_next(token, io);
 }
@@ -874,7 +895,7 @@ size_t sample_scratch_bytes(int V) {
 hipError_t launch_sample(float* logits, int V, float temp, float min_p, float top_p, int top_k,
                          uint64_t* rng_state, void* scratch, const float* pmax, int npart,
                          int* ctl, int* hist, int* out_tokens, const float* embed, int dm,
-                         float* x, hipStream_t s) {
+                         float* x, hipStream_t s, bool gated) {
   if (V < 1 || V > kMaxVocab) return hipErrorInvalidValue;
   if ((uintptr_t)logits % 16) return hipErrorInvalidValue;  // float4 passes
   const SampleParams p{temp, min_p, top_p, top_k};
@@ -885,12 +906,12 @@ hipError_t launch_sample(float* logits, int V, float temp, float min_p, float to
   }
   if (!pmax) {
     hipLaunchKernelGGL(k_samp_scale, dim3(kFront), dim3(kFrontThreads), 0, s, logits, V, temp,
-                       scratch);
+                       scratch, gated ? (const int*)ctl : nullptr);
     pmax = scratch_of(scratch, V).pmax;
     npart = kFront;
   }
   hipLaunchKernelGGL(k_samp_hist, dim3(kFront), dim3(kFrontThreads), 0, s, logits, V, p, scratch,
-                     pmax, npart);
+                     pmax, npart, gated ? (const int*)ctl : nullptr);
   hipLaunchKernelGGL(k_sample, dim3(1), dim3(kThreads), 0, s, logits, V, p, rng_state, scratch,
                      pmax, npart, io);
   return hipGetLastError();
@@ -909,7 +930,8 @@ extern "C" int bm_hip_sample_advanced(float* logits, int vocab, float temp, floa
   }
   const hipError_t e =
       bm::launch_sample(logits, vocab, temp, min_p, top_p, top_k, rng, workspace, nullptr, 0,
-                        nullptr, nullptr, token_out, nullptr, 0, nullptr, (hipStream_t)stream);
+                        nullptr, nullptr, token_out, nullptr, 0, nullptr, (hipStream_t)stream,
+                        false);
   if (e != hipSuccess) {
     bm_set_error("sample_advanced: %s (vocab %d, logits %p; vocab 1..256000, 16-byte aligned logits)",
                  hipGetErrorString(e), vocab, (void*)logits);

@@ -395,12 +395,15 @@ int bm_hip_model_set_layer_state(bm_hip_model_t *m,
  * synchronization.  Writes the tokens; *decode_ms = device time of the
  * steps (prefill excluded, as the reference's tok/s).  Returns the number of
  * tokens (cut after the first 50256 or 0 when stop_on_eos), -1 on error.
- * stop_on_eos only cuts the returned list: all n_steps steps run on the
- * device, so the recurrent state, ring position, history, logits and
- * sampler state are left n_steps past the prompt, where the reference's
- * loop (src/main.c:498) stops stepping at the end token.  A caller that
- * continues after an end token restarts from its own state (reset +
- * prefill, or bm_hip_model_state_load). */
+ * With stop_on_eos the step that picks the end token is the last that
+ * changes anything, as in the reference's loop (src/main.c:473-500): the
+ * recurrent state, ring position, history, logits and sampler state stay
+ * where that step left them although the device replays the step graph
+ * n_steps times (a done word in the control block turns the later steps'
+ * stores off).  This holds for d_model and d_inner multiples of 64 up to
+ * 8192 (the fused step kernels); other widths run all n_steps and only the
+ * returned list is cut.  bm_hip_model_decode and bm_hip_model_step then
+ * continue from the end token. */
 int bm_hip_model_generate(bm_hip_model_t *m,
                           const int32_t *prompt,
                           int n_prompt,
@@ -409,8 +412,9 @@ int bm_hip_model_generate(bm_hip_model_t *m,
                           int stop_on_eos,
                           int32_t *out_tokens,
                           double *decode_ms);
-/* n_steps more steps from the current device state; tokens
- * readable with bm_hip_model_tokens. */
+/* n_steps more steps from the current device state (also after a
+ * generate that stopped at an end token); tokens readable with
+ * bm_hip_model_tokens. */
 int bm_hip_model_decode(bm_hip_model_t *m,
                         int n_steps,
                         float penalty,

@@ -332,6 +332,58 @@ def test_prefill_lengths_vs_oracle(hip):
         m.free()
 
 
+def test_generate_stops_at_end_token(hip):
+    """generate with stop_on_eos against the reference's loop, which stops
+    stepping at the end token (src/main.c:473-500): the returned tokens end
+    with it, and the recurrent state, ring position and logits are those of
+    the step that picked it, although the device replayed the step graph for
+    all n_steps.  A device-resident continuation (decode) then goes on from
+    the end token as the reference would.  Model: vocabulary 64, d_model
+    128, 2 layers, 4 heads (seed 3), whose greedy stream picks token 0, an
+    end token, at step 8."""
+    blob = bh.synth_model(64, 128, 2, 4, 3, bh.SYNTH_UNIFORM)
+    prompt = bh.synth_prompt(3, 64, 6)
+    note("generate stop_on_eos, vocab 64 d_model 128")
+    O, h = _oracle_model(blob)
+    m = bh.Model(blob)
+    try:
+        toks, _ = m.generate(prompt, 24, stop_on_eos=True)
+        p = np.ascontiguousarray(prompt[:-1], np.int32)
+        O.orc_model_prefill(h, ptr(p), p.size)
+        hist, cur, ref = [int(t) for t in prompt], int(prompt[-1]), []
+        while len(ref) < 24:
+            harr = np.array(hist[-256:], np.int32)
+            cur = O.orc_model_step(h, cur, ptr(harr), harr.size, 1.0)
+            ref.append(cur)
+            hist.append(cur)
+            if cur in (0, 50256):
+                break
+        assert ref[-1] == 0 and len(ref) == 9, ref
+        assert toks.tolist() == ref
+        for layer in range(m.n_layers):
+            cs, ss, pos = m.layer_state(layer)
+            ocs = np.empty((3, m.d_inner), np.float32)
+            oss = np.empty(m.d_inner, np.float32)
+            assert pos == O.orc_model_layer_state(h, layer, ptr(ocs), ptr(oss))
+            same_bits(cs, ocs, "conv_state[%d]" % layer)
+            same_bits(ss, oss, "ssm_state[%d]" % layer)
+        same_bits(m.logits(), np.ctypeslib.as_array(O.orc_model_logits(h), (m.vocab,)),
+                  "logits of the end token's step")
+        m.decode(4)
+        cont = []
+        for _ in range(4):
+            harr = np.array(hist[-256:], np.int32)
+            cur = O.orc_model_step(h, cur, ptr(harr), harr.size, 1.0)
+            cont.append(cur)
+            hist.append(cur)
+        assert m.tokens(4).tolist() == cont
+        same_bits(m.logits(), np.ctypeslib.as_array(O.orc_model_logits(h), (m.vocab,)),
+                  "logits after the continuation")
+    finally:
+        O.orc_model_free(h)
+        m.free()
+
+
 def test_tiny_generate_matches_reference(hip):
     g = gold("tiny")
     blob, prompt, steps = model_image(g)
