@@ -642,27 +642,6 @@ def leg_roofline(L, reps=5):
                 rows_per_launch=N)
 
 
-DECODE_PROFILE = os.path.join(ROOT, "profiles", "decode_1b_kernels.txt")
-
-
-def decode_kernel_avg_us(name):
-    """Average duration of a decode kernel from the committed rocprofv3
-    summary of the same decode (its kernel-stats table)."""
-    try:
-        lines = open(DECODE_PROFILE).read().splitlines()
-    except OSError:
-        return None
-    for line in lines:
-        f = line.split()
-        if name in line and len(f) > 5:
-            try:
-                int(f[-5])
-                return float(f[-4])
-            except ValueError:
-                continue
-    return None
-
-
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_per_launch.txt")
 PROFILE_FILES = {
     "decode": os.path.join(ROOT, "profiles", "decode_1b_kernels.txt"),
@@ -711,14 +690,15 @@ def roofline_obj(kernel, key, which, bytes_per_launch, us, note):
 def roofline_decode(c, dev_ms_per_step):
     """The headline decode against HBM: the packed weight bytes of one token
     over the device time of a step, and its dominant kernel (the in_proj +
-    SSM kernel: a layer's in_proj rows per launch) from the profile."""
+    SSM kernel: a layer's in_proj rows per launch) at its average duration
+    in the decode phase of the committed profile."""
     dm, di, nh = c["d_model"], 2 * c["d_model"], c["n_heads"]
     bpt = packed_bytes_per_token(c)
     ach = bpt / (dev_ms_per_step * 1e-3) / 1e9
     r = dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
              frac=round(ach / HBM_PEAK_GBPS, 4), bytes_per_token=bpt,
              device_ms_per_step=dev_ms_per_step)
-    avg = decode_kernel_avg_us("k_inproj_ssm")
+    avg = profile_avg_us("decode", "k_inproj_ssm")
     if avg:
         inproj_bytes = (2 * di + 3 * nh) * dm // 4
         k_ach = inproj_bytes / (avg * 1e-6) / 1e9
