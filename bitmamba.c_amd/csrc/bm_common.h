@@ -65,6 +65,11 @@ enum { MODE_STORE = 0, MODE_ACC = 1, MODE_I32 = 2 };
 hipError_t launch_product(const uint8_t *act, const float *scale_x, int M,
                           const uint8_t *packed, int N, int K, float w_scale,
                           bool canonical, void *out, int mode, hipStream_t s);
+// int8 activations straight into the few-token MFMA product (exact int32
+// totals, no workspace): hipErrorNotSupported unless the product takes that
+// kernel and every row of xq starts on 16 bytes
+hipError_t launch_small_i8(const int8_t *xq, int M, int ldx, int K, const uint8_t *packed, int N,
+                           bool canonical, int32_t *out, hipStream_t s);
 bool product_needs_generic(int M, int K);
 bool product_reads_nibbles(int M, int N, int K);
 hipError_t launch_generic(const int8_t *xq, int ldx, const float *scale_x,

@@ -795,13 +795,13 @@ __device__ __forceinline__ int dot64c(uint4 w, const uint32_t (&xa)[16]) {
                xa);
 }
 
-template <int T, int P, int NPF, bool CANON>
-__global__ __launch_bounds__(256) void k_rows_i8(const int8_t* __restrict__ xq, int ldx, int K,
+template <int T, int P, int NPF, bool CANON, bool XVEC, int NW>
+__global__ __launch_bounds__(64 * NW) void k_rows_i8(const int8_t* __restrict__ xq, int ldx, int K,
                                                  const uint8_t* __restrict__ W, int N,
                                                  int32_t* __restrict__ out) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t nib[];  // [K / 4]
+  extern __shared__ __attribute__((aligned(16))) uint32_t nib[];  // [K / 4 + 4]
   constexpr int RPW = 64 / T;
-  constexpr int XG = 2;  // 16-column groups per thread: K / 16 <= 512
+  constexpr int XG = (512 + 64 * NW - 1) / (64 * NW);  // 16-column groups per thread: K / 16 <= 512
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int u = lane % T, sub = lane / T, unit_base = sub * T;
   const int G = (N + RPW - 1) / RPW;
@@ -812,45 +812,48 @@ __global__ __launch_bounds__(256) void k_rows_i8(const int8_t* __restrict__ xq, 
   const size_t wstride = (size_t)(K >> 2);
   const int chunks = K >> 6, n_groups = K >> 4;
 
-  // the token's int8 values first (16 columns per group)
+  // The token's int8 values first (16 columns per group), then the weight
+  // rows.  Every load is issued unconditionally (indices clamped into the
+  // buffers, unused values replaced by zeros afterwards): a load inside a
+  // branch makes the compiler wait for all outstanding loads at the branch's
+  // end, so the conversion of x would wait for every weight byte instead of
+  // running while the rows are in flight.
   const int8_t* __restrict__ xr = xq + (size_t)m * ldx;
-  const bool vec = ((uintptr_t)xr & 15) == 0;
   uint4 xv[XG];
 #pragma unroll
   for (int i = 0; i < XG; ++i) {
-    const int g = tid + i * (int)blockDim.x;
-    xv[i] = make_uint4(0, 0, 0, 0);
-    if (g < n_groups) {
-      if (vec) {
-        xv[i] = *(const uint4*)(xr + 16 * g);
-      } else {
-        uint32_t wd[4] = {0, 0, 0, 0};
+    const int g = min(tid + i * (int)blockDim.x, n_groups - 1);
+    if constexpr (XVEC) {
+      xv[i] = *(const uint4*)(xr + 16 * g);
+    } else {
+      uint32_t wd[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < 16; ++j) wd[j >> 2] |= (uint32_t)(uint8_t)xr[16 * g + j] << (8 * (j & 3));
-        xv[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-      }
+      for (int j = 0; j < 16; ++j) wd[j >> 2] |= (uint32_t)(uint8_t)xr[16 * g + j] << (8 * (j & 3));
+      xv[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
     }
   }
 
   uint4 wv[NPF][P];
 #pragma unroll
   for (int it = 0; it < NPF; ++it) {
-    const int grp = g0 + wave + 4 * it;
+    const int grp = g0 + wave + NW * it;
     const int r = grp * RPW + sub;
+    const int rc = min(r, N - 1);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int j = p * T + u;
-      wv[it][p] = (grp < g1 && r < N && j < chunks)
-                      ? load_stream16(W + (size_t)r * wstride + 16 * j)
-                      : make_uint4(0, 0, 0, 0);
+      const uint4 w = load_stream16(W + (size_t)rc * wstride + 16 * min(j, chunks - 1));
+      wv[it][p] = (grp < g1 && r < N && j < chunks) ? w : make_uint4(0, 0, 0, 0);
     }
   }
 
-  // split nibbles of the token's values into LDS
+  // split nibbles of the token's values into LDS (groups past K go to a
+  // spare slot, so that the stores, and with them the loads, stay
+  // unconditional)
 #pragma unroll
   for (int i = 0; i < XG; ++i) {
-    const int g = tid + i * (int)blockDim.x;
-    if (g < n_groups) *(uint4*)(nib + 4 * g) = split_nibbles16(xv[i]);
+    const int g = min(tid + i * (int)blockDim.x, n_groups);
+    *(uint4*)(nib + 4 * g) = split_nibbles16(xv[i]);
   }
   __syncthreads();
 
@@ -881,14 +884,14 @@ __global__ __launch_bounds__(256) void k_rows_i8(const int8_t* __restrict__ xq, 
   int32_t* __restrict__ orow = out + (size_t)m * N;
 #pragma unroll
   for (int it = 0; it < NPF; ++it) {
-    const int grp = g0 + wave + 4 * it;
+    const int grp = g0 + wave + NW * it;
     if (grp < g1) {  // uniform per wave
       const int t = total(wv[it]);
       const int r = grp * RPW + sub;
       if (u == 0 && r < N) orow[r] = t;
     }
   }
-  for (int grp = g0 + wave + 4 * NPF; grp < g1; grp += 4) {  // beyond the prefetch
+  for (int grp = g0 + wave + NW * NPF; grp < g1; grp += NW) {  // beyond the prefetch
     const int r = grp * RPW + sub;
     uint4 w[P];
 #pragma unroll
@@ -1274,17 +1277,27 @@ hipError_t launch_rows_dev(const float* x, int K, const float* gamma, const uint
 
 bool rows_i8_fit(int K) { return K % 64 == 0 && K <= 8192; }  // K / 16 <= 2 * 256 groups
 
-template <int T, int P, int NPF>
+template <int T, int P, int NPF, int NW = 4>
 static hipError_t rows_i8_t(const int8_t* xq, int M, int ldx, int K, const uint8_t* W, int N,
                             bool canonical, int32_t* out, hipStream_t s) {
   const int rpw = 64 / T;
   const int G = (N + rpw - 1) / rpw;
-  const dim3 grid((unsigned)max(1, (G + 4 * NPF - 1) / (4 * NPF)), (unsigned)M), block(256);
-  const size_t lds = (size_t)K;  // K / 4 dwords of split nibbles
-  if (canonical)
-    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, true>), grid, block, lds, s, xq, ldx, K, W, N, out);
+  const dim3 grid((unsigned)max(1, (G + NW * NPF - 1) / (NW * NPF)), (unsigned)M), block(64 * NW);
+  const size_t lds = (size_t)K + 16;  // K / 4 dwords of split nibbles + a spare group
+  // every token's row starts on 16 bytes: 16-byte loads of x
+  const bool xvec = ((uintptr_t)xq & 15) == 0 && (M == 1 || ldx % 16 == 0);
+  if (canonical && xvec)
+    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, true, true, NW>), grid, block, lds, s, xq, ldx, K, W,
+                       N, out);
+  else if (canonical)
+    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, true, false, NW>), grid, block, lds, s, xq, ldx, K,
+                       W, N, out);
+  else if (xvec)
+    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, false, true, NW>), grid, block, lds, s, xq, ldx, K,
+                       W, N, out);
   else
-    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, false>), grid, block, lds, s, xq, ldx, K, W, N, out);
+    hipLaunchKernelGGL((k_rows_i8<T, P, NPF, false, false, NW>), grid, block, lds, s, xq, ldx, K,
+                       W, N, out);
   return hipGetLastError();
 }
 
@@ -1294,10 +1307,11 @@ hipError_t launch_rows_i8(const int8_t* xq, int M, int ldx, int K, const uint8_t
   if (K <= 1024) return rows_i8_t<16, 1, 4>(xq, M, ldx, K, W, N, canonical, out, s);
   if (K <= 2048) return rows_i8_t<32, 1, 4>(xq, M, ldx, K, W, N, canonical, out, s);
   if (K <= 4096) return rows_i8_t<64, 1, 4>(xq, M, ldx, K, W, N, canonical, out, s);
-  // K = N = 8192, M = 1 (stress shape, weights cold): 6.5 us with two row
-  // groups per wave (1024 blocks), 7.1 with four, 7.7 with eight, 7.5 with
-  // 32 lanes per row
-  return rows_i8_t<64, 2, 2>(xq, M, ldx, K, W, N, canonical, out, s);
+  // K = N = 8192, M = 1 (stress shape, weights cold, per call with launch
+  // gaps): 5.8 us with four row groups per wave (512 blocks of 4 waves);
+  // 6.0 with two (1024 blocks), 6.3 with five or eight, 6.4 with one;
+  // 6.1-6.9 with blocks of 8 or 16 waves, 6.4-8.7 with blocks of 2
+  return rows_i8_t<64, 2, 4>(xq, M, ldx, K, W, N, canonical, out, s);
 }
 
 // in_proj + SSM for every head: y (and the states) updated in one launch

@@ -550,16 +550,15 @@ __global__ __launch_bounds__(256) void k_gemv_mt(const uint8_t* __restrict__ act
 // ---------------------------------------------------------------------------
 // Few-token product on int8 MFMA (2 <= M <= 256, K % 128 == 0): block row
 // y takes tokens 32y .. 32y+31, the 32 rows of v_mfma_i32_32x32x32_i8's A
-// operand (rows past M are zeros and are not stored); 32 weight rows are
-// its B operand.  A block
-// of 8 waves owns GPB groups of 32 weight rows; the WPG waves of a group
-// split its 1024-column slices.  Each wave loads a slice's packed weights
-// and the tokens' permuted int8 (cache-resident: every block reads them)
-// with coalesced loads, regroups them for the MFMA lanes through its own
-// LDS, decodes the weights in registers, and leaves one fp32 term
-// per (slice, token, row) in LDS -- (x.code - sum x) / (scale_x * w_scale),
-// exact int32 before the one rounding -- which the block then folds in slice
-// order (src/kernel.c:255-256, 407-425).  Lane (j, h) covers columns
+// operand (rows past M are not stored); 32 weight rows are its B operand.
+// A block of 8 waves owns GPB groups of 32 weight rows; the WPG waves of a
+// group split its 1024-column slices.  Each wave loads a slice's packed
+// weights and the tokens' permuted int8 (cache-resident: every block reads
+// them) with coalesced loads, regroups them for the MFMA lanes through its
+// own LDS, decodes the weights in registers, and leaves the exact int32
+// x.code per (slice, token, row) in LDS; the block then folds the slices in
+// order, each as (x.code - sum x) / (scale_x * w_scale) with one rounding
+// (src/kernel.c:255-256, 407-425).  Lane (j, h) covers columns
 // 128t + 64h + 16q .. in step q of each 128-column block t.
 // ---------------------------------------------------------------------------
 constexpr int kSmMaxM = 32, kSmMaxSlices = 16;  // K <= 16384
@@ -569,7 +568,25 @@ __host__ __device__ inline int sm_wpg(int n_slices) {  // waves per row group: a
   return n_slices >= 8 ? 8 : (n_slices >= 4 ? 4 : (n_slices >= 2 ? 2 : 1));
 }
 
-template <bool CANON, int MODE>
+// 16 int8 values in column order -> the MFMA operand order of the
+// activation workspace (byte 4k+b = column 4b+k): a 4x4 byte transpose
+__device__ __forceinline__ v4i transpose_4x4_bytes(v4i c) {
+  const uint32_t c0 = c[0], c1 = c[1], c2 = c[2], c3 = c[3];
+  // v_perm_b32 selector bytes: 0..3 = bytes of the second operand, 4..7 of
+  // the first
+  const uint32_t t0 = __builtin_amdgcn_perm(c1, c0, 0x05010400u);  // c0.0 c1.0 c0.1 c1.1
+  const uint32_t t1 = __builtin_amdgcn_perm(c3, c2, 0x05010400u);  // c2.0 c3.0 c2.1 c3.1
+  const uint32_t t2 = __builtin_amdgcn_perm(c1, c0, 0x07030602u);  // c0.2 c1.2 c0.3 c1.3
+  const uint32_t t3 = __builtin_amdgcn_perm(c3, c2, 0x07030602u);  // c2.2 c3.2 c2.3 c3.3
+  return v4i{(int)__builtin_amdgcn_perm(t1, t0, 0x05040100u), (int)__builtin_amdgcn_perm(t1, t0, 0x07060302u),
+             (int)__builtin_amdgcn_perm(t3, t2, 0x05040100u), (int)__builtin_amdgcn_perm(t3, t2, 0x07060302u)};
+}
+
+// RAW: act is the callers' int8 activations themselves (row stride
+// act_stride, rows on 16 bytes, int32 outputs): each wave puts its chunks in
+// operand order and sums its slice's values (sdot4 against ones) itself, so
+// no preparation launch and no workspace are needed.
+template <bool CANON, int MODE, int MT8, bool RAW>
 __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ act,
                                                     size_t act_stride,
                                                     const float* __restrict__ scale_x, int M,
@@ -577,10 +594,12 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
                                                     float w_scale, float* __restrict__ out,
                                                     int32_t* __restrict__ out_i32) {
   constexpr bool I32 = MODE == 2;
-  // token tile blockIdx.y: tokens 32y .. 32y+31
+  // token tile blockIdx.y: tokens 32y .. 32y+31, of which the first 8 * MT8
+  // are loaded (the tile's rows past M repeat its last token; their results
+  // are never stored)
   const int m_base = blockIdx.y * kSmMaxM;
   act += (size_t)m_base * act_stride;
-  scale_x += m_base;
+  if (!I32) scale_x += m_base;
   if (I32)
     out_i32 += (size_t)m_base * N;
   else
@@ -598,14 +617,21 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
   const int wpg = sm_wpg(n_slices), gpb = 8 / wpg, spw = (n_slices + wpg - 1) / wpg;
   const int rows_b = 32 * gpb;
   const size_t wstride = (size_t)(K >> 2);
-  const size_t perm = act_perm_off(K);
+  const size_t perm = RAW ? 0 : act_perm_off(K);
+  static_assert(!RAW || MODE == 2, "raw int8 activations: int32 outputs only");
 
-  for (int i = tid; i < kSmMaxM * n_slices; i += 512) {
-    const int m = i / n_slices, sl = i % n_slices;
-    s_sx[m][sl] = ((const int*)(act + (size_t)min(m, M - 1) * act_stride))[sl];
-  }
-  if (tid < kSmMaxM) s_inv[tid] = I32 ? 0.0f : inv_scale_of(scale_x[min(tid, M - 1)], w_scale);
-  __syncthreads();
+  // Every global load below is unconditional (indices clamped into the
+  // buffers; values that are not needed are never used): a load inside a
+  // branch makes the compiler wait for all outstanding loads at its first
+  // use, so the first step would wait for the whole slice.  The slice sums
+  // of x and the scales are needed only by the fold: loaded first, into
+  // registers, and put in LDS after the products.
+  const int e_sx = min(tid, kSmMaxM * n_slices - 1);
+  const int sx_m = e_sx / n_slices, sx_sl = e_sx % n_slices;
+  int sx_v = 0;
+  if constexpr (!RAW) sx_v = ((const int*)(act + (size_t)min(sx_m, M - 1) * act_stride))[sx_sl];
+  float sc_v = 0.0f;
+  if constexpr (!I32) sc_v = scale_x[min(tid & (kSmMaxM - 1), M - 1)];
 
   const int g = wave / wpg;                       // row group in the block
   const int n0 = (blockIdx.x * gpb + g) * 32;     // its first weight row
@@ -631,64 +657,96 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
     // run), then moved to the MFMA lanes through the wave's own LDS.
     const int nst = (kb1 - kb0) >> 7;  // 128-column blocks, <= 8
     const int wb = (kb1 - kb0) >> 2;   // packed bytes of the slice per row
-    v4i ca[kSlice / 128][4], cb[kSlice / 512][4];
-#pragma unroll
-    for (int t = 0; t < kSlice / 128; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = cr + 8 * i;
-        ca[t][i] = (t < nst && m < M)
-                       ? *(const v4i*)(act + (size_t)m * act_stride + perm + kb0 + 128 * t + 16 * cc)
-                       : v4i{0, 0, 0, 0};
-      }
-#pragma unroll
-    for (int u = 0; u < kSlice / 512; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = min(n0 + cr + 8 * i, N - 1);
-        const int off = 128 * u + 16 * cc;
-        cb[u][i] = off < wb ? *(const v4i*)(W + (size_t)r * wstride + (kb0 >> 2) + off)
-                            : v4i{0, 0, 0, 0};
-      }
+    // Issued in the order the steps use them (B of steps 0-3, A of step 0,
+    // ..., B of steps 4-7, A of step 4, ...), held there by scheduling
+    // barriers: completion waits count loads in issue order, so a step
+    // waits only for its own operands and those issued before them.
+    v4i ca[kSlice / 128][MT8], cb[kSlice / 512][4];
 #pragma unroll
     for (int t = 0; t < kSlice / 128; ++t) {
-      if (t < nst) {
+      if (t % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          *(v4i*)(tA + swz(cr + 8 * i, cc)) = ca[t][i];
-          if (t % 4 == 0) *(v4i*)(tB + swz(cr + 8 * i, cc)) = cb[t / 4][i];
-        }
-        wave_lds_sync();
-        const uint4 bw = *(const uint4*)(tB + swz(j32, 2 * (t % 4) + h));
-        v4i ao[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ao[q] = *(const v4i*)(tA + swz(j32, 4 * h + q));
-        wave_lds_sync();  // the reads are done before the next step's writes
-        const uint32_t w4[4] = {bw.x, bw.y, bw.z, bw.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t pw = CANON ? w4[q] : canon_codes(w4[q]);
-          v4i bo;
-          bo[0] = (int)(pw & 0x03030303u);
-          bo[1] = (int)((pw >> 2) & 0x03030303u);
-          bo[2] = (int)((pw >> 4) & 0x03030303u);
-          bo[3] = (int)((pw >> 6) & 0x03030303u);
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao[q], bo, acc, 0, 0, 0);
+          const int r = min(n0 + cr + 8 * i, N - 1);
+          cb[t / 4][i] = *(const v4i*)(W + (size_t)r * wstride + (kb0 >> 2) +
+                                       min(32 * t + 16 * cc, wb - 16));
         }
       }
+#pragma unroll
+      for (int i = 0; i < MT8; ++i)
+        ca[t][i] = *(const v4i*)(act + (size_t)min(cr + 8 * i, M - 1) * act_stride + perm + kb0 +
+                                 128 * min(t, nst - 1) + 16 * cc);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // acc element v: token 8(v/4) + 4h + v%4, weight row j32
+    // Every step runs (a branch around a step would pull its loads into
+    // the branch); the steps past a short last slice multiply zero codes.
+    int xs[MT8];
+#pragma unroll
+    for (int i = 0; i < MT8; ++i) xs[i] = 0;
+#pragma unroll
+    for (int t = 0; t < kSlice / 128; ++t) {
+      if constexpr (RAW) {
+#pragma unroll
+        for (int i = 0; i < MT8; ++i) {
+          const v4i c = ca[t][i];
+          int sum = 0;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) sum = __builtin_amdgcn_sdot4(c[d], 0x01010101, sum, false);
+          xs[i] += t < nst ? sum : 0;
+          ca[t][i] = transpose_4x4_bytes(c);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i < MT8) *(v4i*)(tA + swz(cr + 8 * i, cc)) = ca[t][i];
+        if (t % 4 == 0) *(v4i*)(tB + swz(cr + 8 * i, cc)) = cb[t / 4][i];
+      }
+      wave_lds_sync();
+      uint4 bw = *(const uint4*)(tB + swz(j32, 2 * (t % 4) + h));
+      if (t >= nst) bw = make_uint4(0, 0, 0, 0);
+      v4i ao[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ao[q] = *(const v4i*)(tA + swz(j32, 4 * h + q));
+      wave_lds_sync();  // the reads are done before the next step's writes
+      const uint32_t w4[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pw = CANON ? w4[q] : canon_codes(w4[q]);
+        v4i bo;
+        bo[0] = (int)(pw & 0x03030303u);
+        bo[1] = (int)((pw >> 2) & 0x03030303u);
+        bo[2] = (int)((pw >> 4) & 0x03030303u);
+        bo[3] = (int)((pw >> 6) & 0x03030303u);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao[q], bo, acc, 0, 0, 0);
+      }
+    }
+    if constexpr (RAW) {
+      // the slice's sum of x for token cr + 8i: over the 8 lanes cr*8 .. +7
+#pragma unroll
+      for (int i = 0; i < MT8; ++i) {
+        int v = xs[i];
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        v += __shfl_xor(v, 4);
+        if (cc == 0) s_sx[cr + 8 * i][sl] = v;
+      }
+    }
+    // acc element v: token 8(v/4) + 4h + v%4, weight row j32; the exact
+    // int32 x.code of the slice (rows of A past 8 MT8 hold stale bytes and
+    // only reach tokens that are never stored)
     float* __restrict__ part = s_part + (size_t)sl * kSmMaxM * rows_b;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int m = 8 * (v >> 2) + 4 * h + (v & 3);
-      const int t = acc[v] - s_sx[m][sl];
-      part[m * rows_b + g * 32 + j32] =
-          I32 ? __int_as_float(t) : __fmul_rn((float)t, s_inv[m]);
+      part[m * rows_b + g * 32 + j32] = __int_as_float(acc[v]);
     }
   }
+  if (!RAW && tid < kSmMaxM * n_slices) s_sx[sx_m][sx_sl] = sx_v;
+  if (!I32 && tid < kSmMaxM) s_inv[tid] = inv_scale_of(sc_v, w_scale);
   __syncthreads();
-  // fold the slices in order: thread -> (token, row) pairs
+  // fold the slices in order: thread -> (token, row) pairs; each slice's
+  // term is (x.code - sum x) / (scale_x * w_scale), exact int32 before the
+  // one rounding (src/kernel.c:255-256, 407-425)
   for (int i = tid; i < M * rows_b; i += 512) {
     const int m = i / rows_b, r = i % rows_b;
     const int row = blockIdx.x * rows_b + r;
@@ -696,11 +754,11 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
     float o = 0.0f;
     int tot = 0;
     for (int sl = 0; sl < n_slices; ++sl) {
-      const float f = s_part[((size_t)sl * kSmMaxM + m) * rows_b + r];
+      const int t = __float_as_int(s_part[((size_t)sl * kSmMaxM + m) * rows_b + r]) - s_sx[m][sl];
       if (I32)
-        tot += __float_as_int(f);
+        tot += t;
       else
-        o = __fadd_rn(o, f);
+        o = __fadd_rn(o, __fmul_rn((float)t, s_inv[m]));
     }
     const size_t at = (size_t)m * N + row;
     if (I32)
@@ -1346,12 +1404,51 @@ static hipError_t product_t(const uint8_t* act, const float* scale_x, int M, con
     const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
     const dim3 grid((N + 32 * gpb - 1) / (32 * gpb), (M + kSmMaxM - 1) / kSmMaxM);
     const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
-    hipLaunchKernelGGL((k_gemm_small<CANON, MODE>), grid, dim3(512), lds, s, act,
-                       act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
-                       (int32_t*)out);
+    // 8-token groups of A that a block loads: what its tile of up to 32
+    // tokens needs
+    if (M <= 8)
+      hipLaunchKernelGGL((k_gemm_small<CANON, MODE, 1, false>), grid, dim3(512), lds, s, act,
+                         act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                         (int32_t*)out);
+    else if (M <= 16)
+      hipLaunchKernelGGL((k_gemm_small<CANON, MODE, 2, false>), grid, dim3(512), lds, s, act,
+                         act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                         (int32_t*)out);
+    else
+      hipLaunchKernelGGL((k_gemm_small<CANON, MODE, 4, false>), grid, dim3(512), lds, s, act,
+                         act_row_bytes(K), scale_x, M, W, N, K, w_scale, (float*)out,
+                         (int32_t*)out);
     return hipGetLastError();
   }
   return gemv_dispatch<CANON, MODE>(act, scale_x, M, W, N, K, w_scale, out, s);
+}
+
+template <bool CANON, int MT8>
+static void small_i8_t(dim3 grid, size_t lds, const int8_t* xq, int M, int ldx, int K,
+                       const uint8_t* W, int N, int32_t* out, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemm_small<CANON, MODE_I32, MT8, true>), grid, dim3(512), lds, s,
+                     (const uint8_t*)xq, (size_t)ldx, (const float*)nullptr, M, W, N, K, 0.0f,
+                     (float*)nullptr, out);
+}
+
+hipError_t launch_small_i8(const int8_t* xq, int M, int ldx, int K, const uint8_t* packed, int N,
+                           bool canonical, int32_t* out, hipStream_t s) {
+  if (product_path(M, N, K) != 3 || ((uintptr_t)xq & 15) != 0 || ldx % 16 != 0)
+    return hipErrorNotSupported;
+  const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
+  const dim3 grid((N + 32 * gpb - 1) / (32 * gpb), (M + kSmMaxM - 1) / kSmMaxM);
+  const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
+  const int mt8 = M <= 8 ? 1 : (M <= 16 ? 2 : 4);
+  if (canonical) {
+    if (mt8 == 1) small_i8_t<true, 1>(grid, lds, xq, M, ldx, K, packed, N, out, s);
+    else if (mt8 == 2) small_i8_t<true, 2>(grid, lds, xq, M, ldx, K, packed, N, out, s);
+    else small_i8_t<true, 4>(grid, lds, xq, M, ldx, K, packed, N, out, s);
+  } else {
+    if (mt8 == 1) small_i8_t<false, 1>(grid, lds, xq, M, ldx, K, packed, N, out, s);
+    else if (mt8 == 2) small_i8_t<false, 2>(grid, lds, xq, M, ldx, K, packed, N, out, s);
+    else small_i8_t<false, 4>(grid, lds, xq, M, ldx, K, packed, N, out, s);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_product(const uint8_t* act, const float* scale_x, int M, const uint8_t* packed,

@@ -763,6 +763,15 @@ extern "C" int bm_hip_ternary_gemm_i32_dev(const int8_t* xq, int M, int ldx,
     BM_HIP_CHECK_RET(bm::launch_rows_i8(xq, M, ldx, K, packed, N, canonical != 0, out, s), -1);
     return 0;
   }
+  {
+    // few tokens: one launch that reads the int8 rows itself
+    const hipError_t e = bm::launch_small_i8(xq, M, ldx, K, packed, N, canonical != 0, out, s);
+    if (e == hipSuccess) return 0;
+    if (e != hipErrorNotSupported) {
+      bm_set_error("%s", hipGetErrorString(e));
+      return -1;
+    }
+  }
   BM_HIP_CHECK_RET(bm::launch_prep_i8(xq, M, ldx, K, (uint8_t*)act,
                                       bm::product_reads_nibbles(M, N, K), s),
                    -1);

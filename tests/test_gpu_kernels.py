@@ -180,6 +180,9 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    (1100, 1024, 700), (48, 16384, 96), (2, 2048, 77),
                                    (31, 4096, 300), (5, 8192, 33), (97, 4096, 200),
                                    (256, 2048, 64),
+                                   # few tokens with a short last 1024-column slice
+                                   # (1, 3 and 1 blocks of 128 columns)
+                                   (7, 1152, 100), (20, 1408, 70), (9, 3200, 40),
                                    # GEMM tiles 32x128 (700x2048x1100, 1100x1024x700), 64x128
                                    # (300x1152x260 and 2100x128x2048 in 128-deep stages,
                                    # 1233x256x8512 and 1920x256x8512 in 256-deep ones);
