@@ -122,10 +122,12 @@ def leg_decode(L, steps, warmup, sampled=False, fast=False):
     L.bm_hip_synchronize()
     wall = time.perf_counter() - t0
     toks = np.concatenate([first, m.tokens(steps)])
-    # the step's kernels one at a time (layer 0, launched back to back on
-    # the model's stream between events): the roofline's live durations
-    ktimes = {name: round(m.time_kernel(which, 0, 200), 3) for name, which in
-              (("k_inproj_ssm", 0), ("out_proj", 1), ("lm_head", 2))}
+    # the step's kernels one kind at a time, launched back to back on the
+    # model's stream between events (the layers in turn, 240 launches, so
+    # that each reads weights the previous launches did not, as in a step;
+    # the one LM head 200 times): the roofline's live durations
+    ktimes = {name: round(m.time_kernel(which, layer, reps), 3) for name, which, layer, reps in
+              (("k_inproj_ssm", 0, -1, 240), ("out_proj", 1, -1, 240), ("lm_head", 2, 0, 200))}
     m.reset()
     samp = None
     if sampled:
@@ -1336,16 +1338,16 @@ def main():
             "k_inproj_ssm (1B in_proj 2048->8384: RMSNorm + int8 + GEMV + the SSM step of its "
             "heads, one launch per layer)", "k_inproj_ssm", "decode", (2 * di + 3 * nh) * dm // 4,
             kt["k_inproj_ssm"],
-            "dominant kernel of the headline decode; bytes: the layer's packed in_proj weights; "
-            "avg_us: 200 launches back to back on the model's stream between HIP events "
-            "(bm_hip_model_time_kernel, layer 0)")
+            "dominant kernel of the headline decode; bytes: a layer's packed in_proj weights; "
+            "avg_us: 240 launches back to back on the model's stream between HIP events, the "
+            "24 layers in turn (bm_hip_model_time_kernel)")
         rd = roofline_decode(c, line["device_ms_per_step"])
         rd["kernels"] = {
             "k_inproj_ssm": line["roofline"],
             "out_proj": roofline_obj(
                 "k_rows_fused, out_proj form (1B out_proj 4096->2048: RMSNorm + int8 + GEMV + "
                 "residual)",
-                "out_proj", "decode", di * dm // 4, kt["out_proj"], "layer 0, live"),
+                "out_proj", "decode", di * dm // 4, kt["out_proj"], "the layers in turn, live"),
             "lm_head": roofline_obj(
                 "k_rows_fused, LM head form (final norm + LM head 2048->50257 + greedy "
                 "candidates)", "lm_head", "decode", c["vocab"] * dm // 4, kt["lm_head"],

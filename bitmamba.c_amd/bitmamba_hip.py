@@ -311,7 +311,8 @@ class Model:
 
     def time_kernel(self, which, layer=0, reps=50):
         """Average microseconds per launch of one decode kernel (0 in_proj +
-        SSM, 1 out_proj, 2 LM head); changes the state: reset afterwards."""
+        SSM, 1 out_proj, 2 LM head) of `layer`, or of the layers in turn
+        (layer -1); changes the state: reset afterwards."""
         us = C.c_float(0.0)
         check(lib().bm_hip_model_time_kernel(self.h, which, layer, reps, C.byref(us)),
               "time_kernel")

@@ -962,7 +962,7 @@ extern "C" int bm_hip_model_set_fast(bm_hip_model_t* m, int on) {
 // (greedy candidates).  Changes the recurrent state and the activations.
 extern "C" int bm_hip_model_time_kernel(bm_hip_model_t* m, int which, int layer, int reps,
                                         float* avg_us) {
-  if (!m || !avg_us || reps < 1 || which < 0 || which > 2 || layer < 0 || layer >= m->nl) {
+  if (!m || !avg_us || reps < 1 || which < 0 || which > 2 || layer < -1 || layer >= m->nl) {
     bm_set_error("bm_hip_model_time_kernel: bad arguments");
     return -1;
   }
@@ -971,11 +971,14 @@ extern "C" int bm_hip_model_time_kernel(bm_hip_model_t* m, int which, int layer,
     bm_set_error("bm_hip_model_time_kernel: the model's widths take the generic kernels");
     return -1;
   }
-  const Layer& Ly = m->L[layer];
-  float* cs = m->conv_state + (size_t)layer * 3 * di;
-  float* ss = m->ssm_state + (size_t)layer * di;
   hipStream_t s = m->stream;
+  int next = 0;  // layer == -1: the layers in turn, as a decode step reads them
   auto launch = [&]() -> hipError_t {
+    const int li = layer >= 0 ? layer : next;
+    next = next + 1 == m->nl ? 0 : next + 1;
+    const Layer& Ly = m->L[li];
+    float* cs = m->conv_state + (size_t)li * 3 * di;
+    float* ss = m->ssm_state + (size_t)li * di;
     if (which == 0)
       return bm::launch_inproj_ssm(m->x, dm, Ly.in_norm, Ly.in_proj, Ly.in_scale, m->nh, m->hd,
                                    Ly.dt_bias, Ly.A, Ly.conv_wt, Ly.conv_b, cs, ss, Ly.D, m->y,

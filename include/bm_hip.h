@@ -318,7 +318,9 @@ int bm_hip_model_set_fast(bm_hip_model_t *m, int on);
  * profiles): one kernel of the decode step, launched reps times back to
  * back on the model's stream after two untimed launches, timed with events
  * on that stream.  which: 0 = in_proj + SSM step of `layer`, 1 = out_proj
- * (+ residual) of `layer`, 2 = the LM head (greedy candidates).  Writes the
+ * (+ residual) of `layer`, 2 = the LM head (greedy candidates); layer -1
+ * takes the layers in turn (0, 1, .., n_layers - 1, 0, ..), so that each
+ * launch reads weights that the previous launches did not.  Writes the
  * average microseconds per launch to *avg_us.  The recurrent state and the
  * activations change: reset the model (or load a saved state) afterwards.
  * 0, or -1 (bm_hip_last_error) for bad arguments or widths that take the
