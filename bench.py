@@ -585,8 +585,9 @@ def leg_stress(L, reps=10):
             b.free()
     for c in cold:
         c.free()
-    out["note"] = ("M=1: one launch (k_rows_i8); M=16: k_prep_i8 + k_gemm_small; M=4096: "
-                   "k_prep_i8 + k_gemm; canonical=0 (code 11 handled in-kernel); warm: "
+    out["note"] = ("M=1: one launch (k_rows_i8); M=16: one launch (k_gemm_small reading the "
+                   "int8 rows itself); M=4096: k_prep_i8 + k_gemm; canonical=0 (code 11 "
+                   "handled in-kernel); warm: "
                    "the one 16.8 MB weight tensor stays cache-resident across calls; cold: 32 "
                    "copies (537 MB) used in turn, so each call streams its weights from HBM")
     wb = N * K // 4
@@ -596,10 +597,10 @@ def leg_stress(L, reps=10):
         "bytes: packed weights + int8 input + int32 output; avg_us: HIP events over 64 "
         "back-to-back calls on cold weights")
     out["roofline_m16_cold"] = roofline_obj(
-        "k_prep_i8 + k_gemm_small (M=16)", "stress_m16", "stress",
+        "k_gemm_small, int8-row form (M=16 on int8 MFMA, one launch)", "stress_m16", "stress",
         wb + 16 * K + 4 * 16 * N, out["M16"]["cold_us"],
-        "bytes: packed weights + int8 inputs + int32 outputs; avg_us: both launches of a call, "
-        "HIP events over 64 calls on cold weights")
+        "bytes: packed weights + int8 inputs + int32 outputs; avg_us: HIP events over 64 "
+        "back-to-back calls on cold weights")
     return out
 
 
