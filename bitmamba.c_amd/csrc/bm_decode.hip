@@ -18,6 +18,8 @@
 // dependent add per element, while the block's weight rows are already in
 // flight.  All elementwise prologue work runs on register-resident copies of
 // the input.  Kernel boundaries order the phases; no grid-wide fences.
+#include <type_traits>
+
 #include "bm_dev.h"
 #include "bm_libm.h"
 
@@ -366,6 +368,20 @@ __device__ float split_prologue(SplitIn<G, PRENORM>& in, const Lds& l, bool fast
     rms = fast_rms<G>(xv, l);
   } else {
     put_squares<G>(xv, l);
+    if constexpr (!std::is_same<std::decay_t<F>, NoWork>::value) {
+      // waves 1.. issue their rows during the chain: the other inputs are
+      // passed through an empty asm first (which waits for them now), so
+      // that their uses after the chain depend on this point and not on
+      // loads that the compiler, not knowing how many rows were issued in
+      // between, would otherwise wait for with all of the rows
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        asm volatile("" : "+v"(xv[k].x), "+v"(xv[k].y), "+v"(xv[k].z), "+v"(xv[k].w));
+        asm volatile("" : "+v"(in.gv[k].x), "+v"(in.gv[k].y), "+v"(in.gv[k].z), "+v"(in.gv[k].w));
+        if constexpr (PRENORM)
+          asm volatile("" : "+v"(in.gp[k].x), "+v"(in.gp[k].y), "+v"(in.gp[k].z), "+v"(in.gp[k].w));
+      }
+    }
     rms = chain_rms<G>(l, idle);
   }
   if constexpr (PRENORM) {
@@ -540,8 +556,12 @@ struct DropOut {
   float* scale;     // scale_x, written by block 0 (or null)
 };
 
+// FASTC: 0 = the fast argument decides at run time; 1 / 2 = parity / fast
+// mode fixed at compile time (the LM head: with both prologues in one kernel
+// the compiler's merge of the two paths made waves 1.. wait for all the rows
+// they issue during the first chain before the second norm could start)
 template <int T, int P, int NPF, int C, bool PRENORM, int MODE, int PICK, bool WP,
-          bool DROP = false>
+          bool DROP = false, int FASTC = 0>
 __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x, int K,
                                                     const float* __restrict__ gamma_pre,
                                                     const float* __restrict__ gamma,
@@ -623,9 +643,11 @@ __global__ __launch_bounds__(256) void k_rows_fused(const float* __restrict__ x,
   float scale_x;
   if constexpr (WP) {
     if constexpr (defer_rows)
-      scale_x = split_prologue<C, PRENORM>(sin, l, fast != 0, xn_out, xq_out, load_rows);
+      scale_x = split_prologue<C, PRENORM>(sin, l, FASTC == 0 ? fast != 0 : FASTC == 2, xn_out,
+                                           xq_out, load_rows);
     else
-      scale_x = split_prologue<C, PRENORM>(sin, l, fast != 0, xn_out, xq_out);
+      scale_x = split_prologue<C, PRENORM>(sin, l, FASTC == 0 ? fast != 0 : FASTC == 2, xn_out,
+                                           xq_out);
   } else {
     float rms = pro_rms<C>(sx, K, l);
     if constexpr (PRENORM) {
@@ -1134,7 +1156,25 @@ __global__ __launch_bounds__(256) void k_pick(const float* __restrict__ part_v,
   const int done = tid == 0 ? ctl[CTL_DONE] : 0;
   float bv = -1e9f;
   int bi = 0x7fffffff;
-  for (int b = tid; b < n_parts; b += blockDim.x) {
+  // the first 4 * 256 candidates in one round of loads (indices clamped,
+  // unconditional: a load in a branch would make the first comparison wait
+  // for the loads of every turn), the rest in turns
+  constexpr int PU = 4;
+  float pv[PU];
+  int pi[PU];
+#pragma unroll
+  for (int u = 0; u < PU; ++u) {
+    const int b = min(tid + 256 * u, n_parts - 1);
+    pv[u] = part_v[b];
+    pi[u] = part_i[b];
+  }
+#pragma unroll
+  for (int u = 0; u < PU; ++u)
+    if (tid + 256 * u < n_parts && (pv[u] > bv || (pv[u] == bv && pi[u] < bi))) {
+      bv = pv[u];
+      bi = pi[u];
+    }
+  for (int b = tid + 256 * PU; b < n_parts; b += blockDim.x) {
     const float v = part_v[b];
     const int i = part_i[b];
     if (v > bv || (v == bv && i < bi)) {
@@ -1218,6 +1258,24 @@ static hipError_t rows_t(const float* x, int K, const float* gpre, const float* 
   const size_t lds = lds_bytes(K);
   const dim3 grid(rows_blocks<NPF>(N, K)), block(256);
   if (K % 64 != 0) return hipErrorInvalidValue;
+  if constexpr (PRENORM && !DROP) {
+    // the LM head: parity and fast mode as separate kernels
+    if (K == 1024 || K == 2048) {
+      if (K == 1024 && fast)
+        hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true, DROP, 2>), grid,
+                           block, lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, 1, dr);
+      else if (K == 1024)
+        hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true, DROP, 1>), grid,
+                           block, lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, 0, dr);
+      else if (fast)
+        hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true, DROP, 2>), grid,
+                           block, lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, 1, dr);
+      else
+        hipLaunchKernelGGL((k_rows_fused<32, 1, NPF, 2, PRENORM, MODE, PICK, true, DROP, 1>), grid,
+                           block, lds, s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, 0, dr);
+      return hipGetLastError();
+    }
+  }
   if (K == 1024)
     hipLaunchKernelGGL((k_rows_fused<16, 1, NPF, 1, PRENORM, MODE, PICK, true, DROP>), grid, block, lds,
                        s, x, K, gpre, g, W, N, w_scale, out, pv, pi, temp, (int)fast, dr);
