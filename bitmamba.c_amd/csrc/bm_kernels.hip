@@ -680,11 +680,15 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
     }
     // Every step runs (a branch around a step would pull its loads into
     // the branch); the steps past a short last slice multiply zero codes.
+    // Software-pipelined: a step's operands are read from LDS into
+    // registers one step ahead, so the wave's LDS buffers are free again as
+    // soon as those reads complete; each turn issues step t's MFMAs first,
+    // then stages step t+1 (its loads' wait, the write to LDS, the read
+    // back) while they run.
     int xs[MT8];
 #pragma unroll
     for (int i = 0; i < MT8; ++i) xs[i] = 0;
-#pragma unroll
-    for (int t = 0; t < kSlice / 128; ++t) {
+    auto stage_write = [&](int t) __attribute__((always_inline)) {
       if constexpr (RAW) {
 #pragma unroll
         for (int i = 0; i < MT8; ++i) {
@@ -701,13 +705,22 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
         if (i < MT8) *(v4i*)(tA + swz(cr + 8 * i, cc)) = ca[t][i];
         if (t % 4 == 0) *(v4i*)(tB + swz(cr + 8 * i, cc)) = cb[t / 4][i];
       }
-      wave_lds_sync();
-      uint4 bw = *(const uint4*)(tB + swz(j32, 2 * (t % 4) + h));
-      if (t >= nst) bw = make_uint4(0, 0, 0, 0);
-      v4i ao[4];
+    };
+    uint4 bwv[2];
+    v4i aov[2][4];
+    auto stage_read = [&](int t) __attribute__((always_inline)) {
+      bwv[t & 1] = *(const uint4*)(tB + swz(j32, 2 * (t % 4) + h));
+      if (t >= nst) bwv[t & 1] = make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ao[q] = *(const v4i*)(tA + swz(j32, 4 * h + q));
-      wave_lds_sync();  // the reads are done before the next step's writes
+      for (int q = 0; q < 4; ++q) aov[t & 1][q] = *(const v4i*)(tA + swz(j32, 4 * h + q));
+    };
+    stage_write(0);
+    wave_lds_sync();
+    stage_read(0);
+    wave_lds_sync();  // the reads are done before the next step's writes
+#pragma unroll
+    for (int t = 0; t < kSlice / 128; ++t) {
+      const uint4 bw = bwv[t & 1];
       const uint32_t w4[4] = {bw.x, bw.y, bw.z, bw.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -717,7 +730,13 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
         bo[1] = (int)((pw >> 2) & 0x03030303u);
         bo[2] = (int)((pw >> 4) & 0x03030303u);
         bo[3] = (int)((pw >> 6) & 0x03030303u);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao[q], bo, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(aov[t & 1][q], bo, acc, 0, 0, 0);
+      }
+      if (t + 1 < kSlice / 128) {
+        stage_write(t + 1);
+        wave_lds_sync();
+        stage_read(t + 1);
+        wave_lds_sync();
       }
     }
     if constexpr (RAW) {
