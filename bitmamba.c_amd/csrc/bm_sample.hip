@@ -132,9 +132,18 @@ __device__ __forceinline__ int cvtt_x86(float f) {
 __device__ __forceinline__ float front_max(const float* __restrict__ pmax, int n) {
   const int lane = threadIdx.x & 63;
   float v = -1e30f;
-  for (int i = lane; i < n; i += 64) {
-    const float w = pmax[i];
-    if (w > v) v = w;
+  // the first 8 * 64 maxima in one round of loads (indices clamped,
+  // unconditional: loads in the loop would each wait for the one before)
+  constexpr int FU = 8;
+  float w[FU];
+#pragma unroll
+  for (int u = 0; u < FU; ++u) w[u] = pmax[min(lane + 64 * u, n - 1)];
+#pragma unroll
+  for (int u = 0; u < FU; ++u)
+    if (lane + 64 * u < n && w[u] > v) v = w[u];
+  for (int i = lane + 64 * FU; i < n; i += 64) {
+    const float x = pmax[i];
+    if (x > v) v = x;
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -237,10 +246,18 @@ __device__ int gather(const Scratch& sc, const int (&pc)[kListsPerWave], int seg
   constexpr int NW = kThreads / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int cnt = 0;
+  // the first 64 entries of every list in one round of loads (index 0 of
+  // an empty list is in bounds: a segment holds at least 4), kept for the
+  // second pass; the rest in turns
+  Cand first[kListsPerWave];
+#pragma unroll
+  for (int j = 0; j < kListsPerWave; ++j)
+    first[j] = (sc.pre + (size_t)(wave * kListsPerWave + j) * seg)[min(lane, max(pc[j], 1) - 1)];
 #pragma unroll
   for (int j = 0; j < kListsPerWave; ++j) {
     const Cand* src = sc.pre + (size_t)(wave * kListsPerWave + j) * seg;
-    for (int i = lane; i < pc[j]; i += 64) cnt += src[i].val >= thr;
+    cnt += lane < pc[j] && first[j].val >= thr;
+    for (int i = lane + 64; i < pc[j]; i += 64) cnt += src[i].val >= thr;
   }
   cnt = wave_sum_i32(cnt);
   if (lane == 0) sm.ired[wave] = cnt;
@@ -260,7 +277,10 @@ __device__ int gather(const Scratch& sc, const int (&pc)[kListsPerWave], int seg
     for (int i0 = 0; i0 < pc[j]; i0 += 64) {
       const int i = i0 + lane;
       Cand x{0, 0.0f};
-      if (i < pc[j]) x = src[i];
+      if (i0 == 0)
+        x = first[j];
+      else if (i < pc[j])
+        x = src[i];
       const bool h = i < pc[j] && x.val >= thr;
       const uint64_t m = __ballot(h);
       if (h) dst[off + __popcll(m & below)] = x;
