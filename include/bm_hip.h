@@ -262,8 +262,10 @@ size_t bm_hip_noalloc_scratch_bytes(void);
 /* Exact int32 product of int8 activations and ternary weights:
  * out[m*N + r] = sum_k xq[m*ldx + k] * decode(W[r][k]) (stress shape;
  * activations need no quantization).  M = 1 (K % 64 == 0, K <= 8192) runs
- * as one GEMV launch that reads xq itself and leaves `act` untouched; larger
- * M the int8 MFMA GEMM.  Needs bm_hip_i8_act_bytes(M, K) bytes of `act`. */
+ * as one GEMV launch that reads xq itself and leaves `act` untouched; few
+ * tokens (K % 128 == 0, rows of xq on 16 bytes) one int8 MFMA launch that
+ * also reads xq itself; other shapes prepare `act` first and run the int8
+ * MFMA GEMM.  Needs bm_hip_i8_act_bytes(M, K) bytes of `act`. */
 size_t bm_hip_i8_act_bytes(int M, int K);
 int bm_hip_ternary_gemm_i32_dev(const int8_t *xq,
                                 int M,

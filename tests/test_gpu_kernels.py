@@ -206,6 +206,30 @@ def test_gemm_i32_exact(hip, M, K, N):
     np.testing.assert_array_equal(got, native.orc_gemm_i32(xq, packed, N, K))
 
 
+@pytest.mark.parametrize("M,K,N,off,ldx", [(1, 1024, 300, 1, 1024), (1, 8192, 70, 3, 8192),
+                                            (5, 2048, 200, 0, 2056), (16, 1024, 100, 8, 1032),
+                                            (12, 1152, 90, 0, 1160)])
+def test_gemm_i32_unaligned_rows(hip, M, K, N, off, ldx):
+    """int8 rows that do not start on 16 bytes (a byte offset, or a row
+    stride that is not a multiple of 16): the one-token GEMV reads them byte
+    by byte, the few-token product falls back to the preparation launch;
+    int32 totals exact against the oracle (src/kernel.c:159-316)."""
+    note("gemm i32 unaligned M=%d K=%d N=%d off=%d ldx=%d" % (M, K, N, off, ldx))
+    r = rnd(M * 7 + K + N + off)
+    packed = r.integers(0, 256, (N, K // 4), dtype=np.uint8)
+    xq = r.integers(-128, 128, (M, K), dtype=np.int8)
+    buf = np.zeros(off + M * ldx + 16, np.int8)
+    for m in range(M):
+        buf[off + m * ldx: off + m * ldx + K] = xq[m]
+    dx, dw = DB.from_array(buf), DB.from_array(packed)
+    do, da = DB(4 * M * N), DB(hip.bm_hip_i8_act_bytes(M, K))
+    bh.check(hip.bm_hip_ternary_gemm_i32_dev(dx.ptr + off, M, ldx, dw.ptr, N, K, 0, do.ptr,
+                                             da.ptr, None), "gemm_i32")
+    hip.bm_hip_synchronize()
+    got = do.download((M, N), np.int32)
+    np.testing.assert_array_equal(got, native.orc_gemm_i32(xq, packed, N, K))
+
+
 @pytest.mark.parametrize("M", [1, 16])
 def test_stress_exact_small_m(hip, M):
     """Stress shape K = N = 8192, p(0)=0.6, int8 activations, full check."""
