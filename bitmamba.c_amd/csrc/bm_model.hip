@@ -436,9 +436,11 @@ struct bm_hip_model {
   int top_k = 0;
   uint64_t* rng = nullptr;      // XorShift64* state (src/utils.c:117-134)
   void* samp_scratch = nullptr;
-  // captured decode step
+  // captured decode step, and kGraphSteps of them in one graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  hipGraph_t graph_n = nullptr;
+  hipGraphExec_t exec_n = nullptr;
   float graph_penalty = 1.0f;
   bool graph_with_out = false;
   float graph_samp[4] = {0.0f, 0.0f, 1.0f, 0.0f};
@@ -563,6 +565,21 @@ int enqueue_step(bm_hip_model* m, hipStream_t s, float penalty, bool write_out) 
   return 0;
 }
 
+void drop_graphs(bm_hip_model* m) {
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  if (m->exec_n) (void)hipGraphExecDestroy(m->exec_n);
+  if (m->graph_n) (void)hipGraphDestroy(m->graph_n);
+  m->exec = m->exec_n = nullptr;
+  m->graph = m->graph_n = nullptr;
+}
+
+// decode steps per replay of the multi-step graph: one graph launch per
+// kGraphSteps tokens instead of one per token (every step reads its
+// position, token and counters from the control block on the device, so
+// replaying this graph equals kGraphSteps replays of the one-step graph)
+constexpr int kGraphSteps = 8;
+
 int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
   if (m->no_graph) {
     m->graph_penalty = penalty;
@@ -574,25 +591,23 @@ int ensure_graph(bm_hip_model* m, float penalty, bool write_out) {
       m->graph_fast == m->fast && m->graph_gated == m->gated &&
       memcmp(samp, m->graph_samp, sizeof(samp)) == 0)
     return 0;
-  if (m->exec) {
-    (void)hipGraphExecDestroy(m->exec);
-    m->exec = nullptr;
+  drop_graphs(m);
+  for (int multi = 0; multi < 2; ++multi) {
+    MCHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = 0;
+    for (int i = 0; i < (multi ? kGraphSteps : 1) && rc == 0; ++i)
+      rc = enqueue_step(m, m->stream, penalty, write_out);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc != 0) {
+      if (g) (void)hipGraphDestroy(g);
+      drop_graphs(m);
+      return -1;
+    }
+    MCHECK(e);
+    (multi ? m->graph_n : m->graph) = g;
+    MCHECK(hipGraphInstantiate(multi ? &m->exec_n : &m->exec, g, nullptr, nullptr, 0));
   }
-  if (m->graph) {
-    (void)hipGraphDestroy(m->graph);
-    m->graph = nullptr;
-  }
-  MCHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-  const int rc = enqueue_step(m, m->stream, penalty, write_out);
-  hipGraph_t g = nullptr;
-  const hipError_t e = hipStreamEndCapture(m->stream, &g);
-  if (rc != 0) {
-    if (g) (void)hipGraphDestroy(g);
-    return -1;
-  }
-  MCHECK(e);
-  m->graph = g;
-  MCHECK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
   m->graph_penalty = penalty;
   m->graph_with_out = write_out;
   m->graph_fast = m->fast;
@@ -628,8 +643,7 @@ int ensure_prefill(bm_hip_model* m, int n) {
 void model_release(bm_hip_model* m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
-  if (m->exec) (void)hipGraphExecDestroy(m->exec);
-  if (m->graph) (void)hipGraphDestroy(m->graph);
+  drop_graphs(m);
   for (void* p : {(void*)m->arena, (void*)m->conv_state, (void*)m->ssm_state, (void*)m->ctl,
                   (void*)m->hist, (void*)m->out_tokens, (void*)m->x, (void*)m->proj,
                   (void*)m->y, (void*)m->feat, (void*)m->logits, (void*)m->scale,
@@ -811,26 +825,28 @@ int set_ctl(bm_hip_model* m, int token, const int* history, int history_len, int
   return 0;
 }
 
+// the step graphs write the picked tokens here: room for at least 4096
+// (16 KB), so that a longer generation than the first one does not have to
+// capture the graphs again
 int ensure_out(bm_hip_model* m, int n) {
   if (n <= m->out_cap) return 0;
   if (m->out_tokens) (void)hipFree(m->out_tokens);
   m->out_tokens = nullptr;
   m->out_cap = 0;
-  if (m->exec) {  // the captured graph refers to the old buffer
-    (void)hipGraphExecDestroy(m->exec);
-    (void)hipGraphDestroy(m->graph);
-    m->exec = nullptr;
-    m->graph = nullptr;
-  }
-  MCHECK(hipMalloc(&m->out_tokens, (size_t)n * 4));
-  m->out_cap = n;
+  drop_graphs(m);  // the captured graphs refer to the old buffer
+  const int cap = n > 4096 ? n : 4096;
+  MCHECK(hipMalloc(&m->out_tokens, (size_t)cap * 4));
+  m->out_cap = cap;
   return 0;
 }
 
 // n_steps decode steps back to back on the model stream, timed with events
 int run_steps(bm_hip_model* m, int n_steps, double* decode_ms) {
   MCHECK(hipEventRecord(m->ev0, m->stream));
-  for (int i = 0; i < n_steps; ++i) {
+  int i = 0;
+  if (!m->no_graph)
+    for (; i + kGraphSteps <= n_steps; i += kGraphSteps) MCHECK(hipGraphLaunch(m->exec_n, m->stream));
+  for (; i < n_steps; ++i) {
     if (m->no_graph) {
       if (enqueue_step(m, m->stream, m->graph_penalty, m->graph_with_out)) return -1;
     } else {
