@@ -881,12 +881,10 @@ def cpu_threads():
     """Pool threads of the CPU baseline: one fewer than the CPUs granted
     (affinity mask and cgroup quota), at most 15.  The reference's pool
     spins without yielding in its completion waits and barriers
-    (src/threadpool.c:503-507, 611-614): with as many pool threads as CPUs,
-    any other runnable thread on the box (this process, the harness) takes
-    a CPU from a pool thread and the whole pool waits for it; measured on
-    an 8-CPU host, the 1B decode's 8-thread pool makes no progress for
-    100 s beside four processes that each run 5 ms in 20, while 7 threads
-    decode at 99 tok/s beside them."""
+    (src/threadpool.c:503-507, 611-614), so a pool thread that loses its
+    CPU to another runnable thread (this process's, the runtime's) holds up
+    the whole pool, and a cgroup whose quota equals its CPU count is
+    throttled as soon as anything beside a full pool runs."""
     h = cpu_host()
     n = h["cores_granted"]
     if h["cpu_quota"]:
@@ -1065,6 +1063,14 @@ def thread_states(pid):
                 d = out.setdefault(key, dict(n=0, cpu_ticks=0))
                 d["n"] += 1
                 d["cpu_ticks"] += int(f[11]) + int(f[12])
+                if f[0] != "R":
+                    # where a waiting thread waits: its system call (or -1 for
+                    # a fault) and the mapping its user-space PC lies in
+                    sc = _read(base + "syscall").split()
+                    where = _mapping(pid, int(sc[-1], 16)) if len(sc) >= 3 else ""
+                    d.setdefault("tids", []).append(
+                        "%s start=%s cpu=%d sc=%s %s" % (tid, f[19], int(f[11]) + int(f[12]),
+                                                         " ".join(sc[:2]), where))
             except (OSError, ValueError, IndexError):
                 continue
     except OSError:
@@ -1072,9 +1078,31 @@ def thread_states(pid):
     return out
 
 
+def _read(path):
+    try:
+        return open(path).read().strip()
+    except OSError:
+        return ""
+
+
+def _mapping(pid, pc):
+    """File (and offset in it) of the mapping that holds address pc."""
+    for line in _read("/proc/%d/maps" % pid).splitlines():
+        f = line.split()
+        lo, hi = (int(v, 16) for v in f[0].split("-"))
+        if lo <= pc < hi:
+            return "%s+0x%x" % (os.path.basename(f[5]) if len(f) > 5 else "anon",
+                                pc - lo + int(f[2], 16))
+    return "pc=0x%x" % pc
+
+
 def dropin_child(threads):
     """The drop-in decode leg in a process of its own (its spin-wait pool
     never shares a process with the other legs); prints "DROPIN {json}"."""
+    import faulthandler
+    import signal
+    # the watchdog asks a silent child for its Python stacks before it stops it
+    faulthandler.register(signal.SIGUSR1, all_threads=True)
     L = bh.lib()
     if not L.bm_hip_init():
         sys.exit("bm_hip_init: " + bh.last_error())
@@ -1085,6 +1113,7 @@ def run_dropin(threads, stall_s=60.0, total_s=300.0):
     """dropin_child, watched like the CPU suite: a child that prints nothing
     for stall_s is killed and run again once with half the threads; the
     result records the stalls."""
+    import signal
     import subprocess
     import threading
     stalls = []
@@ -1092,9 +1121,7 @@ def run_dropin(threads, stall_s=60.0, total_s=300.0):
     for t in (threads, max(1, threads // 2)):
         cmd = [sys.executable, os.path.abspath(__file__), "--dropin-child", str(t)]
         # one OpenMP thread: the child's only OpenMP work is writing the
-        # synthetic model file, and an idle 16-thread OpenMP pool beside
-        # the reference's pool and the HIP runtime's threads was followed
-        # by a pool worker that never started (thread_states)
+        # synthetic model file
         env = dict(os.environ, OMP_NUM_THREADS="1")
         proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, text=True, bufsize=1, env=env)
         lines, last = [], [time.time()]
@@ -1112,6 +1139,11 @@ def run_dropin(threads, stall_s=60.0, total_s=300.0):
             time.sleep(0.2)
             if time.time() - last[0] > stall_s or time.time() - start > total_s:
                 threads_seen = thread_states(proc.pid)
+                try:
+                    os.kill(proc.pid, signal.SIGUSR1)  # Python stacks to stderr
+                    time.sleep(1.0)
+                except OSError:
+                    pass
                 proc.kill()
                 killed = True
                 proc.wait()

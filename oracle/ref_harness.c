@@ -26,8 +26,12 @@ static int32_t *g_lut_buf;
  * on this CPU (AVX2+FMA on x86-64). */
 const char *bmref_init(int threads, int kind)
 {
-    bm_set_threads(threads);
+    /* the wait policy is set before any worker exists: a worker reads it in
+     * its idle loop (src/threadpool.c:183-206), and one that has not run yet
+     * must not start under a policy other than the one the pool dispatches
+     * with */
     bm_set_poll(0);
+    bm_set_threads(threads);
     dispatch_init();
     init_lut();
     if (kind == 0) {
@@ -45,10 +49,19 @@ const char *bmref_init(int threads, int kind)
     return g_kernels.name;
 }
 
-/* pool wait policy: 0 = condvar, 100 = pure spin (the reference default) */
+/* pool wait policy: 0 = condvar, 100 = pure spin (the reference default).
+ * The pool is stopped and started again under the new policy: a worker asleep
+ * on its condvar (poll < 100) is never signalled once the policy is 100,
+ * since a pure-spin dispatch skips the condvars (src/threadpool.c:195-206,
+ * 484-490), so changing the policy under a live pool loses every worker that
+ * slept -- including a worker that had not yet run when the pool was made. */
 void bmref_set_poll(int intensity)
 {
+    int n = bm_get_threads();
+    bm_thread_pool_free();
     bm_set_poll(intensity);
+    if (n > 1)
+        bm_set_threads(n);
 }
 
 void bmref_shutdown(void)
