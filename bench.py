@@ -585,7 +585,7 @@ def leg_stress(L, reps=10):
             b.free()
     for c in cold:
         c.free()
-    out["note"] = ("M=1: one launch (k_rows_i8); M=16: one launch (k_gemm_small reading the "
+    out["note"] = ("M=1: one launch (k_rows_i8); M=16: one launch (k_gemm_few reading the "
                    "int8 rows itself); M=4096: k_prep_i8 + k_gemm; canonical=0 (code 11 "
                    "handled in-kernel); warm: "
                    "the one 16.8 MB weight tensor stays cache-resident across calls; cold: 32 "
@@ -597,7 +597,7 @@ def leg_stress(L, reps=10):
         "bytes: packed weights + int8 input + int32 output; avg_us: HIP events over 64 "
         "back-to-back calls on cold weights")
     out["roofline_m16_cold"] = roofline_obj(
-        "k_gemm_small, int8-row form (M=16 on int8 MFMA, one launch)", "stress_m16", "stress",
+        "k_gemm_few, int8-row form (M=16 on int8 MFMA, one launch)", "stress_m16", "stress",
         wb + 16 * K + 4 * 16 * N, out["M16"]["cold_us"],
         "bytes: packed weights + int8 inputs + int32 outputs; avg_us: HIP events over 64 "
         "back-to-back calls on cold weights")

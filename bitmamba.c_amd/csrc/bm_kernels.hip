@@ -582,6 +582,39 @@ __device__ __forceinline__ v4i transpose_4x4_bytes(v4i c) {
              (int)__builtin_amdgcn_perm(t3, t2, 0x05040100u), (int)__builtin_amdgcn_perm(t3, t2, 0x07060302u)};
 }
 
+// Fold of a few-token block: slice s's exact int32 x.code of (token m, row
+// r) is part[(s * TS + m) * rows_b + r]; each slice's term is
+// (x.code - sum x) / (scale_x * w_scale), exact int32 before the one
+// rounding, added in slice order (src/kernel.c:255-256, 407-425).
+// Thread -> (token, row) pairs of the block's rows.
+template <int MODE, int TS>
+__device__ __forceinline__ void small_fold(const float* __restrict__ s_part,
+                                           const int (*s_sx)[kSmMaxSlices],
+                                           const float* __restrict__ s_inv, int M, int rows_b,
+                                           int N, int n_slices, float* __restrict__ out,
+                                           int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
+  for (int i = threadIdx.x; i < M * rows_b; i += blockDim.x) {
+    const int m = i / rows_b, r = i % rows_b;
+    const int row = blockIdx.x * rows_b + r;
+    if (row >= N) continue;
+    float o = 0.0f;
+    int tot = 0;
+    for (int sl = 0; sl < n_slices; ++sl) {
+      const int t = __float_as_int(s_part[((size_t)sl * TS + m) * rows_b + r]) - s_sx[m][sl];
+      if (I32)
+        tot += t;
+      else
+        o = __fadd_rn(o, __fmul_rn((float)t, s_inv[m]));
+    }
+    const size_t at = (size_t)m * N + row;
+    if (I32)
+      out_i32[at] = tot;
+    else
+      out[at] = MODE == 1 ? __fadd_rn(out[at], o) : o;
+  }
+}
+
 // RAW: act is the callers' int8 activations themselves (row stride
 // act_stride, rows on 16 bytes, int32 outputs): each wave puts its chunks in
 // operand order and sums its slice's values (sdot4 against ones) itself, so
@@ -763,28 +796,182 @@ __global__ __launch_bounds__(512) void k_gemm_small(const uint8_t* __restrict__ 
   if (!RAW && tid < kSmMaxM * n_slices) s_sx[sx_m][sx_sl] = sx_v;
   if (!I32 && tid < kSmMaxM) s_inv[tid] = inv_scale_of(sc_v, w_scale);
   __syncthreads();
-  // fold the slices in order: thread -> (token, row) pairs; each slice's
-  // term is (x.code - sum x) / (scale_x * w_scale), exact int32 before the
-  // one rounding (src/kernel.c:255-256, 407-425)
-  for (int i = tid; i < M * rows_b; i += 512) {
-    const int m = i / rows_b, r = i % rows_b;
-    const int row = blockIdx.x * rows_b + r;
-    if (row >= N) continue;
-    float o = 0.0f;
-    int tot = 0;
-    for (int sl = 0; sl < n_slices; ++sl) {
-      const int t = __float_as_int(s_part[((size_t)sl * kSmMaxM + m) * rows_b + r]) - s_sx[m][sl];
-      if (I32)
-        tot += t;
-      else
-        o = __fadd_rn(o, __fmul_rn((float)t, s_inv[m]));
+  small_fold<MODE, kSmMaxM>(s_part, s_sx, s_inv, M, rows_b, N, n_slices, out, out_i32);
+}
+
+// ---------------------------------------------------------------------------
+// Up to 16 tokens on v_mfma_i32_16x16x64_i8.  The block layout is
+// k_gemm_small's: 8 waves, GPB groups of 32 weight rows, the WPG waves of a
+// group splitting the group's 1024-column slices, the slices folded in order
+// at the end.  In a slice, lane l (i = l % 16, g = l / 16) owns columns
+// 256 s + 64 g .. +63 of super-step s (s = 0..3); MFMA q of the super-step
+// multiplies columns 16 q .. 16 q + 15 of that run (the A and B lanes of one
+// index cover the same columns; D lane l element v is token 4 g + v, row
+// l % 16).  The weights are loaded straight into those lanes (16 packed
+// bytes of rows i and 16 + i per super-step); the slice's activations are
+// loaded coalesced (8 lanes per 128-byte run of a token), put in the wave's
+// own LDS once, and read back in lane order.  Every global load is issued
+// before the first MFMA, activations first, then weights in super-step
+// order, unconditionally (columns past a short last slice read in-bounds
+// bytes and multiply zero codes).  RAW: int8 activations from the caller's
+// rows, put in operand order with a 4x4 byte transpose and summed per slice
+// with v_dot4 against ones.  MT8: 8-token groups loaded (1 for M <= 8; the
+// A rows of tokens not loaded hold stale LDS bytes and reach only tokens
+// that are never stored).  STREAM: nontemporal weight loads, for matrices of
+// 8 MB and more (K = N = 8192 at M = 16: 7.9 against 8.2 us per call with
+// the weights cold; plain loads are faster on smaller matrices and whenever
+// the weights are still cached).
+// ---------------------------------------------------------------------------
+constexpr int kFewM = 16;  // tokens of k_gemm_few
+// K <= 8192: the per-wave activation slices (128 KB) and the slice results
+// (16 KB at most) fit the 160 KB of LDS
+constexpr int kFewMaxSlices = 8;
+inline bool few_stream(int N, int K) { return (size_t)N * (size_t)(K / 4) >= ((size_t)8 << 20); }
+__host__ __device__ inline size_t few_lds(int K) {  // dynamic LDS: the slice results
+  const int n_slices = slices_of(K);
+  return (size_t)n_slices * kFewM * 32 * (8 / sm_wpg(n_slices)) * sizeof(float);
+}
+
+template <bool CANON, int MODE, int MT8, bool RAW, bool STREAM>
+__global__ __launch_bounds__(512) void k_gemm_few(const uint8_t* __restrict__ act,
+                                                  size_t act_stride,
+                                                  const float* __restrict__ scale_x, int M,
+                                                  const uint8_t* __restrict__ W, int N, int K,
+                                                  float w_scale, float* __restrict__ out,
+                                                  int32_t* __restrict__ out_i32) {
+  constexpr bool I32 = MODE == 2;
+  static_assert(!RAW || MODE == 2, "raw int8 activations: int32 outputs only");
+  extern __shared__ __attribute__((aligned(16))) float s_part[];  // [slice][16 tokens][GPB*32 rows]
+  __shared__ int s_sx[kSmMaxM][kSmMaxSlices];
+  __shared__ float s_inv[kSmMaxM];
+  __shared__ __attribute__((aligned(16))) uint8_t s_x[8][kFewM * kSlice];  // per wave: a slice of x
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int cr = lane >> 3, cc = lane & 7;
+  const int n_slices = slices_of(K);
+  const int wpg = sm_wpg(n_slices), gpb = 8 / wpg, spw = (n_slices + wpg - 1) / wpg;
+  const int rows_b = 32 * gpb;
+  const size_t wstride = (size_t)(K >> 2);
+  const size_t perm = RAW ? 0 : act_perm_off(K);
+
+  // fold inputs (slice sums of x, scales): loaded first, into registers
+  const int e_sx = min(tid, kFewM * n_slices - 1);
+  const int sx_m = e_sx / n_slices, sx_sl = e_sx % n_slices;
+  int sx_v = 0;
+  if constexpr (!RAW) sx_v = ((const int*)(act + (size_t)min(sx_m, M - 1) * act_stride))[sx_sl];
+  float sc_v = 0.0f;
+  if constexpr (!I32) sc_v = scale_x[min(tid & (kFewM - 1), M - 1)];
+
+  const int grp = wave / wpg;
+  const int n0 = (blockIdx.x * gpb + grp) * 32;
+  const uint8_t* __restrict__ x0 = act + (size_t)min(cr, M - 1) * act_stride + perm;
+  const uint8_t* __restrict__ x1 = act + (size_t)min(cr + 8, M - 1) * act_stride + perm;
+  const uint8_t* __restrict__ w0 = W + (size_t)min(n0 + li, N - 1) * wstride;
+  const uint8_t* __restrict__ w1 = W + (size_t)min(n0 + 16 + li, N - 1) * wstride;
+  uint8_t* __restrict__ tx = s_x[wave];
+  // 16-byte chunk c of token r's 1024-byte row, XOR-swizzled by r so that
+  // the 16 tokens read at one chunk index hit distinct banks
+  auto xpos = [](int r, int c) __attribute__((always_inline)) { return r * kSlice + 16 * (c ^ r); };
+  auto wave_lds_sync = []() __attribute__((always_inline)) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  const int sl0 = (wave % wpg) * spw, sl1 = min(n_slices, sl0 + spw);
+  for (int sl = sl0; sl < sl1; ++sl) {
+    const int kb0 = sl * kSlice, ncols = min(K, kb0 + kSlice) - kb0;  // a multiple of 128
+    const int nst = ncols >> 7;
+    v4i xa[8][MT8];
+    uint4 wv[4][2];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int c = kb0 + 128 * min(t, nst - 1) + 16 * cc;
+      xa[t][0] = *(const v4i*)(x0 + c);
+      if constexpr (MT8 == 2) xa[t][1] = *(const v4i*)(x1 + c);
     }
-    const size_t at = (size_t)m * N + row;
-    if (I32)
-      out_i32[at] = tot;
-    else
-      out[at] = MODE == 1 ? __fadd_rn(out[at], o) : o;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int c = kb0 + min(256 * st + 64 * lg, ncols - 64);
+      if constexpr (STREAM) {
+        wv[st][0] = load_stream16(w0 + (c >> 2));
+        wv[st][1] = load_stream16(w1 + (c >> 2));
+      } else {
+        wv[st][0] = *(const uint4*)(w0 + (c >> 2));
+        wv[st][1] = *(const uint4*)(w1 + (c >> 2));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the slice's activations into the wave's LDS, in operand order
+    int xs0 = 0, xs1 = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int i = 0; i < MT8; ++i) {
+        v4i a = xa[t][i];
+        if constexpr (RAW) {
+          int sum = 0;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) sum = __builtin_amdgcn_sdot4(a[d], 0x01010101, sum, false);
+          (i == 0 ? xs0 : xs1) += t < nst ? sum : 0;
+          a = transpose_4x4_bytes(a);
+        }
+        *(v4i*)(tx + xpos(cr + 8 * i, 8 * t + cc)) = a;
+      }
+    }
+    // the weights' decode stays below the writes: hoisted above them, it
+    // would make the writes wait for the weight loads
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RAW) {
+      // token cr's (and cr + 8's) slice sum: over the 8 lanes cr*8 .. +7
+      xs0 += __shfl_xor(xs0, 1);
+      xs0 += __shfl_xor(xs0, 2);
+      xs0 += __shfl_xor(xs0, 4);
+      xs1 += __shfl_xor(xs1, 1);
+      xs1 += __shfl_xor(xs1, 2);
+      xs1 += __shfl_xor(xs1, 4);
+      if (cc == 0) {
+        s_sx[cr][sl] = xs0;
+        s_sx[cr + 8][sl] = xs1;
+      }
+    }
+    wave_lds_sync();
+    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const bool valid = 256 * st + 64 * lg < ncols;
+      const uint32_t b0[4] = {wv[st][0].x, wv[st][0].y, wv[st][0].z, wv[st][0].w};
+      const uint32_t b1[4] = {wv[st][1].x, wv[st][1].y, wv[st][1].z, wv[st][1].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const v4i a = *(const v4i*)(tx + xpos(li, 16 * st + 4 * lg + q));
+        const uint32_t p0 = valid ? (CANON ? b0[q] : canon_codes(b0[q])) : 0u;
+        const uint32_t p1 = valid ? (CANON ? b1[q] : canon_codes(b1[q])) : 0u;
+        const v4i o0 = {(int)(p0 & 0x03030303u), (int)((p0 >> 2) & 0x03030303u),
+                        (int)((p0 >> 4) & 0x03030303u), (int)((p0 >> 6) & 0x03030303u)};
+        const v4i o1 = {(int)(p1 & 0x03030303u), (int)((p1 >> 2) & 0x03030303u),
+                        (int)((p1 >> 4) & 0x03030303u), (int)((p1 >> 6) & 0x03030303u)};
+        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, o0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, o1, acc1, 0, 0, 0);
+      }
+      // the next super-step's decode stays below these MFMAs, so that each
+      // super-step waits only for its own weights
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wave_lds_sync();  // the reads are done before the next slice's writes
+    float* __restrict__ part = s_part + (size_t)sl * kFewM * rows_b;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * lg + v;
+      part[m * rows_b + grp * 32 + li] = __int_as_float(acc0[v]);
+      part[m * rows_b + grp * 32 + 16 + li] = __int_as_float(acc1[v]);
+    }
   }
+  if (!RAW && tid < kFewM * n_slices) s_sx[sx_m][sx_sl] = sx_v;
+  if (!I32 && tid < kFewM) s_inv[tid] = inv_scale_of(sc_v, w_scale);
+  __syncthreads();
+  small_fold<MODE, kFewM>(s_part, s_sx, s_inv, M, rows_b, N, n_slices, out, out_i32);
 }
 
 // ---------------------------------------------------------------------------
@@ -1423,6 +1610,23 @@ static hipError_t product_t(const uint8_t* act, const float* scale_x, int M, con
     const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
     const dim3 grid((N + 32 * gpb - 1) / (32 * gpb), (M + kSmMaxM - 1) / kSmMaxM);
     const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
+    if (M <= kFewM && n_slices <= kFewMaxSlices) {
+      const bool big = few_stream(N, K);
+      const size_t fl = few_lds(K), ab = act_row_bytes(K);
+      if (M <= 8 && big)
+        hipLaunchKernelGGL((k_gemm_few<CANON, MODE, 1, false, true>), grid, dim3(512), fl, s, act,
+                           ab, scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+      else if (M <= 8)
+        hipLaunchKernelGGL((k_gemm_few<CANON, MODE, 1, false, false>), grid, dim3(512), fl, s, act,
+                           ab, scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+      else if (big)
+        hipLaunchKernelGGL((k_gemm_few<CANON, MODE, 2, false, true>), grid, dim3(512), fl, s, act,
+                           ab, scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+      else
+        hipLaunchKernelGGL((k_gemm_few<CANON, MODE, 2, false, false>), grid, dim3(512), fl, s, act,
+                           ab, scale_x, M, W, N, K, w_scale, (float*)out, (int32_t*)out);
+      return hipGetLastError();
+    }
     // 8-token groups of A that a block loads: what its tile of up to 32
     // tokens needs
     if (M <= 8)
@@ -1450,6 +1654,19 @@ static void small_i8_t(dim3 grid, size_t lds, const int8_t* xq, int M, int ldx, 
                      (float*)nullptr, out);
 }
 
+template <bool CANON, int MT8>
+static void few_i8_t(dim3 grid, int K, const int8_t* xq, int M, int ldx, const uint8_t* W, int N,
+                     int32_t* out, hipStream_t s) {
+  if (few_stream(N, K))
+    hipLaunchKernelGGL((k_gemm_few<CANON, MODE_I32, MT8, true, true>), grid, dim3(512),
+                       few_lds(K), s, (const uint8_t*)xq, (size_t)ldx, (const float*)nullptr, M,
+                       W, N, K, 0.0f, (float*)nullptr, out);
+  else
+    hipLaunchKernelGGL((k_gemm_few<CANON, MODE_I32, MT8, true, false>), grid, dim3(512),
+                       few_lds(K), s, (const uint8_t*)xq, (size_t)ldx, (const float*)nullptr, M,
+                       W, N, K, 0.0f, (float*)nullptr, out);
+}
+
 hipError_t launch_small_i8(const int8_t* xq, int M, int ldx, int K, const uint8_t* packed, int N,
                            bool canonical, int32_t* out, hipStream_t s) {
   if (product_path(M, N, K) != 3 || ((uintptr_t)xq & 15) != 0 || ldx % 16 != 0)
@@ -1457,6 +1674,16 @@ hipError_t launch_small_i8(const int8_t* xq, int M, int ldx, int K, const uint8_
   const int n_slices = slices_of(K), gpb = 8 / sm_wpg(n_slices);
   const dim3 grid((N + 32 * gpb - 1) / (32 * gpb), (M + kSmMaxM - 1) / kSmMaxM);
   const size_t lds = (size_t)n_slices * kSmMaxM * 32 * gpb * sizeof(float);
+  if (M <= kFewM && n_slices <= kFewMaxSlices) {
+    if (canonical) {
+      if (M <= 8) few_i8_t<true, 1>(grid, K, xq, M, ldx, packed, N, out, s);
+      else few_i8_t<true, 2>(grid, K, xq, M, ldx, packed, N, out, s);
+    } else {
+      if (M <= 8) few_i8_t<false, 1>(grid, K, xq, M, ldx, packed, N, out, s);
+      else few_i8_t<false, 2>(grid, K, xq, M, ldx, packed, N, out, s);
+    }
+    return hipGetLastError();
+  }
   const int mt8 = M <= 8 ? 1 : (M <= 16 ? 2 : 4);
   if (canonical) {
     if (mt8 == 1) small_i8_t<true, 1>(grid, lds, xq, M, ldx, K, packed, N, out, s);

@@ -183,6 +183,9 @@ def test_gemv_i32_exact(hip, K, N, canonical):
                                    # few tokens with a short last 1024-column slice
                                    # (1, 3 and 1 blocks of 128 columns)
                                    (7, 1152, 100), (20, 1408, 70), (9, 3200, 40),
+                                   # up to 16 tokens on 8 MB of weights and more
+                                   # (nontemporal weight loads)
+                                   (11, 4096, 8192), (6, 2048, 16384),
                                    # GEMM tiles 32x128 (700x2048x1100, 1100x1024x700), 64x128
                                    # (300x1152x260 and 2100x128x2048 in 128-deep stages,
                                    # 1233x256x8512 and 1920x256x8512 in 256-deep ones);
@@ -338,6 +341,8 @@ FP_SHAPES = [(1, 1024, 4384), (1, 2048, 8512), (1, 4096, 2048), (1, 2048, 50257)
              # few tokens on MFMA: 1, 2, 3, 4, 5 and 16 slices of 1024 columns
              (7, 2048, 8512), (16, 4096, 2048), (12, 3072, 100), (9, 5120, 64), (31, 1024, 70),
              (30, 16384, 40),
+             # up to 16 tokens on 8 MB of weights and more (nontemporal weight loads)
+             (4, 8192, 4096), (13, 2048, 16384),
              # several token tiles of 32 (ragged last tile), and past the few-token range
              (64, 2048, 8384), (100, 4096, 2048), (256, 4096, 2048), (77, 3072, 96),
              (128, 2048, 8384),
