@@ -237,7 +237,7 @@ def leg_d255m(L, fast=False):
     return r
 
 
-def _dropin_run(L, R, native, path, c, threads, kind, hip):
+def _dropin_run(L, R, native, path, c, threads, kind, hip, tag="255M"):
     """One greedy decode of config c through the reference's own
     model_prefill / model_forward_step, its CPU table of `kind` (0 scalar,
     1 the dispatch_init choice: AVX2) at `threads` pool threads, with the
@@ -257,7 +257,7 @@ def _dropin_run(L, R, native, path, c, threads, kind, hip):
             if R.bmref_use_hip(C.cast(L.bm_hip_register, C.c_void_p)) != 1:
                 raise RuntimeError("bm_hip_register refused the table")
             name = "%s + hip" % name
-        what = "drop-in 255M [%s]" % name
+        what = "drop-in %s [%s]" % (tag, name)
         beat("%s: model loaded" % what)
         prompt = bh.synth_prompt(c["seed"], c["vocab"], c["prompt"])
         p = np.ascontiguousarray(prompt[:-1], np.int32)
@@ -284,7 +284,7 @@ def _dropin_run(L, R, native, path, c, threads, kind, hip):
                       prefill_ms=round(pf_ms, 2), kernels=name, threads=threads)
 
 
-def leg_dropin_255m(L, threads):
+def leg_dropin(L, threads, c, tag, gold_file, calls):
     """The drop-in as a user of the reference runs it: the reference's own
     model_load / model_prefill / model_forward_step (oracle/_ref, built from
     its sources, with its spin-wait thread pool) with its plugin table handed
@@ -292,42 +292,55 @@ def leg_dropin_255m(L, threads):
     file (src/dispatch.c:15-52, src/model.c:840-851): every BitLinear (48
     per token plus the LM head) and the final RMSNorm run through this
     library, one launch each, while ssm_inner, the embedding and the sampler
-    stay on the CPU.  128 greedy steps of the 255M shape, three runs:
+    stay on the CPU.  c["steps"] greedy steps of config c, three runs:
       value: the reference's AVX2 table (its ssm_inner) + this library;
       cpu_same_kernels: the same reference, all on its AVX2 table (its AVX2
         BitLinear differs from its own scalar kernel, which this library
         reproduces, in the last bit of most outputs, so the two streams
         drift apart: first_divergence says where);
       scalar_ssm: the scalar table + this library, whose tokens must be the
-        scalar reference's stream (tests/golden/stream_255m.json).
+        scalar reference's stream (tests/golden/<gold_file>).
     The pool gets one thread fewer than the CPU baseline's: this process's
     main thread also spins (it polls the GPU's completion words), and a
     spin-wait pool that shares its last CPU stalls (see cpu_threads)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import native
-    c = CFG_255M
     R = native.ref()
-    gold_path = os.path.join(ROOT, "tests", "golden", "stream_255m.json")
+    gold_path = os.path.join(ROOT, "tests", "golden", gold_file)
     gold = json.load(open(gold_path)) if os.path.exists(gold_path) else None
     try:
         with tempfile.TemporaryDirectory(dir=tempfile.gettempdir()) as d:
             path = _ref_model_file(c, d)
-            beat("drop-in 255M: model file written")
-            toks, r = _dropin_run(L, R, native, path, c, threads, 1, True)
-            ctoks, cr = _dropin_run(L, R, native, path, c, threads, 1, False)
-            stoks, sr = _dropin_run(L, R, native, path, c, threads, 0, True)
+            beat("drop-in %s: model file written" % tag)
+            toks, r = _dropin_run(L, R, native, path, c, threads, 1, True, tag)
+            ctoks, cr = _dropin_run(L, R, native, path, c, threads, 1, False, tag)
+            stoks, sr = _dropin_run(L, R, native, path, c, threads, 0, True, tag)
     finally:
         R.bmref_shutdown()
     div = next((i for i, (a, b) in enumerate(zip(toks, ctoks)) if a != b), None)
     r.update(steps=c["steps"],
              tokens_match_cpu_same_kernels=toks == ctoks, first_divergence_from_cpu=div,
              cpu_same_kernels=cr,
-             scalar_ssm=dict(sr, tokens_match_reference=(stoks == gold["tokens"]) if gold
-                             else None),
-             calls_per_token="48 BitLinear (in_proj 1024->4192, out_proj 2048->1024) + LM "
-                             "head 1024->50257 + final RMSNorm on the GPU; ssm_inner on "
-                             "the CPU")
+             scalar_ssm=dict(sr, tokens_match_reference=(stoks == gold["tokens"][:len(stoks)])
+                             if gold else None),
+             calls_per_token=calls)
     return r
+
+
+def leg_dropin_255m(L, threads):
+    """leg_dropin at the 255M shape (128 steps)."""
+    return leg_dropin(L, threads, CFG_255M, "255M", "stream_255m.json",
+                      "48 BitLinear (in_proj 1024->4192, out_proj 2048->1024) + LM head "
+                      "1024->50257 + final RMSNorm on the GPU; ssm_inner on the CPU")
+
+
+def leg_dropin_1b(L, threads):
+    """leg_dropin at the 1B shape (64 steps): twice the rows and columns of
+    the 255M shape per BitLinear, so the CPU's time per call grows about
+    fourfold while the GPU's stays near its launch and bus floor."""
+    return leg_dropin(L, threads, dict(CFG_1B, steps=64), "1B", "stream_1b.json",
+                      "48 BitLinear (in_proj 2048->8384, out_proj 4096->2048) + LM head "
+                      "2048->50257 + final RMSNorm on the GPU; ssm_inner on the CPU")
 
 
 def leg_fast_quant(L, M=4096):
@@ -1106,7 +1119,9 @@ def dropin_child(threads):
     L = bh.lib()
     if not L.bm_hip_init():
         sys.exit("bm_hip_init: " + bh.last_error())
-    print("DROPIN " + json.dumps(leg_dropin_255m(L, threads)), flush=True)
+    r = {"255m": leg_dropin_255m(L, threads)}
+    r["1b"] = leg_dropin_1b(L, threads)
+    print("DROPIN " + json.dumps(r), flush=True)
 
 
 def run_dropin(threads, stall_s=60.0, total_s=300.0):
@@ -1154,7 +1169,8 @@ def run_dropin(threads, stall_s=60.0, total_s=300.0):
             if l.startswith("DROPIN "):
                 d = json.loads(l[7:])
                 if stalls:
-                    d["stalls"] = stalls
+                    for v in d.values():
+                        v["stalls"] = stalls
                 return d
         where = [l[2:].strip() for l in lines if l.startswith("P ")]
         stalls.append(dict(threads=t, after=where[-1] if where else "start",
@@ -1327,7 +1343,7 @@ def main():
     # in a child process: it starts the reference's spin-wait pool
     dropin = run_dropin(max(1, cpu_threads() - 1)) if "dropin" in legs else None
     if dropin:
-        log("drop-in decode 255M: %s" % json.dumps(dropin))
+        log("drop-in decode: %s" % json.dumps(dropin))
 
     bpt = packed_bytes_per_token(CFG_1B)
     line = {"metric": METRIC, "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -1398,7 +1414,9 @@ def main():
     line["mfma_ceiling"] = mf
     line["prefill_gemm"] = pre
     line["decode_255m"] = d255
-    line["dropin_decode_255m"] = dropin
+    # a stalled child leaves {"tok_s": None, "stalls": ...} for both shapes
+    line["dropin_decode_255m"] = dropin.get("255m", dropin) if dropin else None
+    line["dropin_decode_1b"] = dropin.get("1b", dropin) if dropin else None
     line["bitlinear_k1024_n4384"] = g1
     line["stress_k8192_n8192"] = strs
     line["vendor_int8_gemm"] = vend
