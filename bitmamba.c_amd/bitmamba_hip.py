@@ -62,6 +62,12 @@ SIGNATURES = {
     "bm_hip_register": (C.c_bool, [C.POINTER(Dispatch)]),
     "bm_hip_bitlinear_forward_batch": (None, [_vp, _i, _i, _vp, _i, _i, _f, _vp, _vp, _vp,
                                               _vp, _i]),
+    "bm_hip_batch_begin": (_vp, [_i, _i, _i, _i, _i]),
+    "bm_hip_batch_ptr": (_vp, [_vp, _i]),
+    "bm_hip_encode_bitlinear": (C.c_bool, [_vp, _i, _i, _vp, _i, _i, _f, _vp, _i]),
+    "bm_hip_encode_residual": (None, [_vp, _i]),
+    "bm_hip_submit_and_wait": (None, [_vp]),
+    "bm_hip_batch_end": (None, [_vp]),
     "bm_hip_malloc": (_vp, [_sz]),
     "bm_hip_free": (None, [_vp]),
     "bm_hip_memcpy_h2d": (_i, [_vp, _vp, _sz]),

@@ -78,6 +78,9 @@ hipError_t launch_generic(const int8_t *xq, int ldx, const float *scale_x,
 hipError_t launch_rms_norm(const float *x, int n, const float *gamma,
                            float *out, float *max_out, hipStream_t s);
 hipError_t launch_canonicalize(uint8_t *p, size_t bytes, hipStream_t s);
+// x[i] += o[i] for i < n, one fp32 rounding each (the residual connection,
+// src/model.c:1140-1142)
+hipError_t launch_residual_add(float *x, const float *o, size_t n, hipStream_t s);
 
 // Host -> device copy of caller memory through the library's own pinned
 // staging (bm_runtime.hip); enqueued on s, complete once s is.

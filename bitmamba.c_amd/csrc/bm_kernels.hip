@@ -1402,6 +1402,12 @@ __global__ void k_canonicalize(uint32_t* __restrict__ p, size_t n_words) {
     p[i] = canon_codes(p[i]);
 }
 
+__global__ void k_residual_add(float* __restrict__ x, const float* __restrict__ o, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    x[i] = __fadd_rn(x[i], o[i]);
+}
+
 __global__ void k_canonicalize_tail(uint8_t* __restrict__ p, size_t n) {
   const size_t i = threadIdx.x;
   if (i < n) p[i] = (uint8_t)canon_codes(p[i]);
@@ -1434,6 +1440,14 @@ hipError_t launch_quantize(const float* x, int M, int n, int x_stride, const flo
   }
   hipLaunchKernelGGL(k_quantize, dim3(M), dim3(QT), 0, s, x, n, x_stride, gamma, x_norm, xq,
                      quant_stride, scale_x, (float*)nullptr, act, act_row_bytes(n));
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_add(float* x, const float* o, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(k_residual_add, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256),
+                     0, s, x, o, n);
   return hipGetLastError();
 }
 

@@ -14,6 +14,7 @@
 
 #include <chrono>
 #include <mutex>
+#include <new>
 #include <unordered_map>
 #include <vector>
 
@@ -70,6 +71,10 @@ struct Backend {
   // (an image registered with bm_hip_set_mmap must not change afterwards)
   std::unordered_map<const void*, Registered> packed;
   std::unordered_map<const void*, Registered> floats;
+  // the last image bm_hip_set_mmap registered: the batch context's tensors
+  // must lie inside it
+  const uint8_t* mmap_base = nullptr;
+  size_t mmap_size = 0;
   // grow-on-demand device scratch for the host-pointer entry points; d_w
   // and d_g receive tensors that belong to no registered image, per call
   DevBuf d_x, d_out, d_act, d_scale, d_w, d_g;
@@ -467,6 +472,8 @@ extern "C" bool bm_hip_set_mmap(const void* base, size_t size) {
   Backend& b = B();
   std::lock_guard<std::mutex> lk(b.mu);
   if (!init_locked(b)) return false;
+  b.mmap_base = (const uint8_t*)base;
+  b.mmap_size = size;
   bm_bit2_view_t v;
   if (bm_bit2_parse(base, size, &v) != 0) {
     // not a BIT2 image: tensors are uploaded lazily on first use
@@ -505,6 +512,8 @@ extern "C" void bm_hip_cleanup(void) {
   for (auto& kv : b.floats) (void)hipFree(kv.second.dev);
   b.packed.clear();
   b.floats.clear();
+  b.mmap_base = nullptr;
+  b.mmap_size = 0;
   for (DevBuf* d : {&b.d_x, &b.d_out, &b.d_act, &b.d_scale, &b.d_w, &b.d_g}) {
     if (d->ptr) (void)hipFree(d->ptr);
     *d = DevBuf{};
@@ -590,6 +599,225 @@ extern "C" bool bm_hip_register(bm_hip_dispatch_t* t) {
   t->bitlinear_row_worker = nullptr;
   t->name = "hip";
   return true;
+}
+
+// ---------------------------------------------------------------------------
+// Batch context (src/metal/bm_metal.h:57-99, src/metal/bm_metal.c:610-960):
+// persistent activation buffers, BitLinear and residual steps encoded
+// without running, and one submit that runs them in order.  Metal shares
+// its buffers with the CPU; here each buffer is a device buffer with a
+// pinned host copy, the pointer bm_hip_batch_ptr returns.  A submit copies
+// to the device what its steps read before any of them writes it (the
+// host copy then holds the caller's latest values), runs the steps on one
+// stream, copies back what they wrote, and waits: at every submit boundary
+// the host copies are what Metal's shared buffers would hold.  Every buffer
+// region a step touches starts at the buffer's first float (n_tokens rows
+// of the step's width), so what a submit reads and writes is a prefix.
+// ---------------------------------------------------------------------------
+struct bm_hip_batch_ctx {
+  struct Op {
+    bool residual;
+    int src, dst, input_dim, rows, cols, count;
+    float w_scale;
+    const uint8_t* dW;
+    const float* dG;
+  };
+  int n_tokens = 0, d_model = 0, max_proj = 0, d_inner = 0, quant_stride = 0;
+  size_t width[4] = {};  // floats per token of X, PROJ, Y, OUT
+  float* host[4] = {};
+  float* dev[4] = {};
+  uint8_t* act = nullptr;  // activation workspace, scales, int8 rows
+  float* scale = nullptr;
+  int8_t* xq = nullptr;
+  std::vector<Op> ops;
+};
+
+namespace {
+
+void batch_free(bm_hip_batch_ctx_t* c) {
+  for (int i = 0; i < 4; ++i) {
+    if (c->host[i]) (void)hipHostFree(c->host[i]);
+    if (c->dev[i]) (void)hipFree(c->dev[i]);
+  }
+  if (c->act) (void)hipFree(c->act);
+  if (c->scale) (void)hipFree(c->scale);
+  if (c->xq) (void)hipFree(c->xq);
+  delete c;
+}
+
+}  // namespace
+
+extern "C" bm_hip_batch_ctx_t* bm_hip_batch_begin(int n_tokens, int d_model, int max_proj,
+                                                  int d_inner, int quant_stride) {
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (!b.ready) {
+    bm_set_error("batch_begin: backend not initialized (bm_hip_init)");
+    return nullptr;
+  }
+  if (n_tokens <= 0 || d_model <= 0 || max_proj <= 0 || d_inner <= 0 || quant_stride < 0) {
+    bm_set_error("batch_begin: invalid dimensions (n_tokens=%d d_model=%d max_proj=%d "
+                 "d_inner=%d)", n_tokens, d_model, max_proj, d_inner);
+    return nullptr;
+  }
+  auto* c = new (std::nothrow) bm_hip_batch_ctx_t();
+  if (!c) return nullptr;
+  c->n_tokens = n_tokens;
+  c->d_model = d_model;
+  c->max_proj = max_proj;
+  c->d_inner = d_inner;
+  c->quant_stride = quant_stride;
+  const size_t widths[4] = {(size_t)d_model, (size_t)max_proj, (size_t)d_inner, (size_t)d_model};
+  const int kmax = d_model > d_inner ? d_model : d_inner;
+  bool ok = true;
+  for (int i = 0; i < 4 && ok; ++i) {
+    c->width[i] = widths[i];
+    const size_t bytes = (size_t)n_tokens * widths[i] * sizeof(float);
+    ok = hipHostMalloc((void**)&c->host[i], bytes, hipHostMallocDefault) == hipSuccess &&
+         hipMalloc((void**)&c->dev[i], bytes) == hipSuccess;
+    if (ok) memset(c->host[i], 0, bytes);
+  }
+  ok = ok && hipMalloc((void**)&c->act, (size_t)n_tokens * bm::act_row_bytes(kmax)) == hipSuccess &&
+       hipMalloc((void**)&c->scale, (size_t)n_tokens * sizeof(float)) == hipSuccess &&
+       hipMalloc((void**)&c->xq, (size_t)n_tokens * kmax) == hipSuccess;
+  if (!ok) {
+    bm_set_error("batch_begin: allocation failed (n_tokens=%d)", n_tokens);
+    batch_free(c);
+    return nullptr;
+  }
+  return c;
+}
+
+extern "C" float* bm_hip_batch_ptr(bm_hip_batch_ctx_t* ctx, int buf_id) {
+  if (!ctx || buf_id < BM_HIP_BUF_X || buf_id > BM_HIP_BUF_OUT) return nullptr;
+  return ctx->host[buf_id];
+}
+
+extern "C" bool bm_hip_encode_bitlinear(bm_hip_batch_ctx_t* ctx, int src_id, int input_dim,
+                                        const uint8_t* packed_data, int rows, int cols,
+                                        float w_scale, const float* norm_weight, int dst_id) {
+  if (!ctx || !packed_data) return false;
+  if ((src_id != BM_HIP_BUF_X && src_id != BM_HIP_BUF_Y) ||
+      (dst_id != BM_HIP_BUF_PROJ && dst_id != BM_HIP_BUF_OUT))
+    return false;
+  if (cols % 16 != 0) {
+    fprintf(stderr, "[HIP] encode: cols=%d not multiple of 16\n", cols);
+    return false;
+  }
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (!b.mmap_base) return false;
+  const uint8_t* w_ptr = packed_data;
+  const uint8_t* n_ptr = (const uint8_t*)norm_weight;
+  const uint8_t* mmap_end = b.mmap_base + b.mmap_size;
+  if (w_ptr < b.mmap_base || n_ptr < b.mmap_base || w_ptr >= mmap_end || n_ptr >= mmap_end) {
+    fprintf(stderr, "[HIP] encode: pointer outside mmap region\n");
+    return false;
+  }
+  const size_t weight_bytes = (size_t)rows * (size_t)((cols + 3) / 4);
+  const size_t norm_bytes = (size_t)input_dim * sizeof(float);
+  if (rows <= 0 || input_dim <= 0 || weight_bytes > (size_t)(mmap_end - w_ptr) ||
+      norm_bytes > (size_t)(mmap_end - n_ptr)) {
+    fprintf(stderr, "[HIP] encode: tensor data exceeds mmap region\n");
+    return false;
+  }
+  // beyond Metal's checks: the norm covers the product's columns, and the
+  // rows fit the buffers (Metal's kernels would run past them)
+  if (input_dim != cols || (size_t)input_dim > ctx->width[src_id] ||
+      (size_t)rows > ctx->width[dst_id]) {
+    fprintf(stderr, "[HIP] encode: input_dim=%d cols=%d rows=%d do not fit the batch buffers\n",
+            input_dim, cols, rows);
+    return false;
+  }
+  const uint8_t* dW = register_packed(b, packed_data, weight_bytes);
+  const float* dG = register_floats(b, norm_weight, (size_t)input_dim);
+  if (!dW || !dG) return false;
+  ctx->ops.push_back(bm_hip_batch_ctx_t::Op{false, src_id, dst_id, input_dim, rows, cols, 0,
+                                            w_scale, dW, dG});
+  return true;
+}
+
+extern "C" void bm_hip_encode_residual(bm_hip_batch_ctx_t* ctx, int count) {
+  if (!ctx) return;
+  if (count < 0 || (size_t)count > (size_t)ctx->n_tokens * ctx->width[BM_HIP_BUF_X]) {
+    fprintf(stderr, "[HIP] encode_residual: count=%d exceeds the batch buffers\n", count);
+    return;
+  }
+  ctx->ops.push_back(bm_hip_batch_ctx_t::Op{true, BM_HIP_BUF_OUT, BM_HIP_BUF_X, 0, 0, 0, count,
+                                            0.0f, nullptr, nullptr});
+}
+
+extern "C" void bm_hip_submit_and_wait(bm_hip_batch_ctx_t* ctx) {
+  if (!ctx) return;
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  // floats of each buffer to copy in (read before this submit writes them)
+  // and to copy back (written)
+  size_t in[4] = {}, out[4] = {}, written[4] = {};
+  auto reads = [&](int id, size_t n) {
+    if (n > written[id] && n > in[id]) in[id] = n;
+  };
+  auto writes = [&](int id, size_t n) {
+    if (n > written[id]) written[id] = n;
+    if (n > out[id]) out[id] = n;
+  };
+  const size_t T = (size_t)ctx->n_tokens;
+  for (const auto& op : ctx->ops) {
+    if (op.residual) {
+      reads(BM_HIP_BUF_X, (size_t)op.count);
+      reads(BM_HIP_BUF_OUT, (size_t)op.count);
+      writes(BM_HIP_BUF_X, (size_t)op.count);
+    } else {
+      reads(op.src, T * op.input_dim);
+      writes(op.dst, T * op.rows);
+    }
+  }
+  hipStream_t s = b.stream;
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 4 && e == hipSuccess; ++i)
+    if (in[i])
+      e = hipMemcpyAsync(ctx->dev[i], ctx->host[i], in[i] * sizeof(float), hipMemcpyHostToDevice,
+                         s);
+  for (const auto& op : ctx->ops) {
+    if (e != hipSuccess) break;
+    if (op.residual) {
+      e = bm::launch_residual_add(ctx->dev[BM_HIP_BUF_X], ctx->dev[BM_HIP_BUF_OUT],
+                                  (size_t)op.count, s);
+      continue;
+    }
+    // each token's row of the source: RMSNorm + int8 (src/kernel.c:72-129,
+    // 356-386), then the blocked product (src/kernel.c:388-447)
+    const int M = ctx->n_tokens, n = op.input_dim;
+    const bool generic = bm::product_needs_generic(M, op.cols);
+    e = bm::launch_quantize(ctx->dev[op.src], M, n, n, op.dG, nullptr, generic ? ctx->xq : nullptr,
+                            n, ctx->scale, generic ? nullptr : ctx->act, s,
+                            !generic && bm::product_reads_nibbles(M, op.rows, op.cols));
+    if (e != hipSuccess) break;
+    if (generic)
+      e = bm::launch_generic(ctx->xq, n, ctx->scale, M, op.dW, op.rows, op.cols, op.w_scale,
+                             ctx->dev[op.dst], bm::MODE_STORE, s);
+    else
+      e = bm::launch_product(ctx->act, ctx->scale, M, op.dW, op.rows, op.cols, op.w_scale, true,
+                             ctx->dev[op.dst], bm::MODE_STORE, s);
+  }
+  for (int i = 0; i < 4 && e == hipSuccess; ++i)
+    if (out[i])
+      e = hipMemcpyAsync(ctx->host[i], ctx->dev[i], out[i] * sizeof(float), hipMemcpyDeviceToHost,
+                         s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  ctx->ops.clear();
+  if (e != hipSuccess) {
+    bm_set_error("%s", hipGetErrorString(e));
+    fprintf(stderr, "[HIP] Batch submit error: %s\n", hipGetErrorString(e));
+  }
+}
+
+extern "C" void bm_hip_batch_end(bm_hip_batch_ctx_t* ctx) {
+  if (!ctx) return;
+  Backend& b = B();
+  std::lock_guard<std::mutex> lk(b.mu);
+  if (b.stream) (void)hipStreamSynchronize(b.stream);
+  batch_free(ctx);
 }
 
 // ---------------------------------------------------------------------------

@@ -136,6 +136,58 @@ void bm_hip_bitlinear_forward_batch(const float *x_batch,
                                     int quant_stride);
 
 /* ------------------------------------------------------------------ */
+/* Batch context: the Metal backend's prefill batching                  */
+/* (src/metal/bm_metal.h:57-99), driven as model_prefill_metal drives   */
+/* it (src/model.c:934-1041).                                           */
+/* ------------------------------------------------------------------ */
+
+/* Buffer ids (BM_BUF_X .. BM_BUF_OUT, src/metal/bm_metal.h:58-63) */
+enum {
+    BM_HIP_BUF_X = 0,    /* n_tokens * d_model floats */
+    BM_HIP_BUF_PROJ = 1, /* n_tokens * max_proj floats */
+    BM_HIP_BUF_Y = 2,    /* n_tokens * d_inner floats */
+    BM_HIP_BUF_OUT = 3,  /* n_tokens * d_model floats */
+};
+typedef struct bm_hip_batch_ctx bm_hip_batch_ctx_t;
+
+/* bm_metal_batch_begin: the four buffers, zeroed.  NULL before bm_hip_init
+ * or on a failed allocation (the caller falls back to the CPU). */
+bm_hip_batch_ctx_t *bm_hip_batch_begin(int n_tokens,
+                                       int d_model,
+                                       int max_proj,
+                                       int d_inner,
+                                       int quant_stride);
+/* bm_metal_batch_ptr: host pointer to a buffer (NULL for another id).  The
+ * buffers live on the device with a pinned host copy: what the caller
+ * writes there before bm_hip_submit_and_wait reaches the steps of that
+ * submit, and what the steps write is there when it returns. */
+float *bm_hip_batch_ptr(bm_hip_batch_ctx_t *ctx, int buf_id);
+/* bm_metal_encode_bitlinear: queue RMSNorm + int8 + the blocked product of
+ * the n_tokens rows of src (X or Y, row stride input_dim) into dst (PROJ or
+ * OUT, row stride rows), bit-exact with scalar_bitlinear_forward_batch
+ * (src/kernel.c:322-338).  Runs nothing.  False, as in Metal, for a bad id,
+ * cols % 16 != 0, no image registered by bm_hip_set_mmap, packed_data or
+ * norm_weight outside it; also when input_dim != cols or the rows do not
+ * fit the buffers. */
+bool bm_hip_encode_bitlinear(bm_hip_batch_ctx_t *ctx,
+                             int src_id,
+                             int input_dim,
+                             const uint8_t *packed_data,
+                             int rows,
+                             int cols,
+                             float w_scale,
+                             const float *norm_weight,
+                             int dst_id);
+/* bm_metal_encode_residual: queue X[i] += OUT[i] for i < count. */
+void bm_hip_encode_residual(bm_hip_batch_ctx_t *ctx, int count);
+/* bm_metal_submit_and_wait: run the queued steps in order and wait; a
+ * failure is reported on stderr ("[HIP] Batch submit error") and in
+ * bm_hip_last_error(). */
+void bm_hip_submit_and_wait(bm_hip_batch_ctx_t *ctx);
+/* bm_metal_batch_end */
+void bm_hip_batch_end(bm_hip_batch_ctx_t *ctx);
+
+/* ------------------------------------------------------------------ */
 /* Device memory helpers (for callers without a HIP runtime of their    */
 /* own; no counterpart in the reference)                                */
 /* ------------------------------------------------------------------ */

@@ -321,3 +321,92 @@ int bmref_model_image(void *h, void **addr, size_t *size)
     *size = m->mmap_size;
     return m->mmap_addr != NULL;
 }
+
+/* ---------------------------------------------------------------------------
+ * model_prefill through the HIP backend's batch context, in the order
+ * model_prefill_metal drives Metal's (src/model.c:934-1041), as a tree built
+ * with HAS_HIP would call it: the embeddings go into the X buffer; the first
+ * submit runs layer 0's in_proj; then, per layer, the CPU scans every
+ * token's SSM step (block_ssm_scan, src/block.c:486-489) and one submit runs
+ * the layer's out_proj, the residual add and the next layer's in_proj.  The
+ * library's entry points come in a table, so that this build does not link
+ * the library.  0, or -1 when the context could not be made or a step was
+ * refused (where the reference would fall back to its CPU prefill).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    bm_hip_batch_ctx_t *(*begin)(int, int, int, int, int);
+    float *(*ptr)(bm_hip_batch_ctx_t *, int);
+    bool (*encode_bitlinear)(bm_hip_batch_ctx_t *, int, int, const uint8_t *,
+                             int, int, float, const float *, int);
+    void (*encode_residual)(bm_hip_batch_ctx_t *, int);
+    void (*submit_and_wait)(bm_hip_batch_ctx_t *);
+    void (*end)(bm_hip_batch_ctx_t *);
+} bmref_batch_api_t;
+
+static bool batch_proj(const bmref_batch_api_t *api,
+                       bm_hip_batch_ctx_t *ctx,
+                       int src,
+                       int dim,
+                       const tensor_t *w,
+                       const tensor_t *norm,
+                       int dst)
+{
+    return api->encode_bitlinear(ctx, src, dim, w->packed_data, w->rows,
+                                 w->cols, w->scale, norm->data, dst);
+}
+
+int bmref_model_prefill_batch(void *h,
+                              const int32_t *tokens,
+                              int n,
+                              const bmref_batch_api_t *api)
+{
+    bitmamba_model_t *m = (bitmamba_model_t *) h;
+    const int d_model = m->config.d_model;
+    const int d_inner = d_model * BM_EXPAND_FACTOR;
+    const int n_layers = m->config.n_layers;
+    int max_proj = 0;
+    for (int i = 0; i < n_layers; i++)
+        if (m->layers[i].in_proj.rows > max_proj)
+            max_proj = m->layers[i].in_proj.rows;
+    bm_hip_batch_ctx_t *ctx =
+        api->begin(n, d_model, max_proj, d_inner, d_inner + 32);
+    if (!ctx)
+        return -1;
+    float *x = api->ptr(ctx, BM_HIP_BUF_X);
+    float *proj = api->ptr(ctx, BM_HIP_BUF_PROJ);
+    float *y = api->ptr(ctx, BM_HIP_BUF_Y);
+    for (int t = 0; t < n; t++) {
+        int tok = tokens[t];
+        if (tok < 0 || tok >= m->config.vocab_size)
+            tok = 0;
+        memcpy(x + (size_t) t * d_model, m->embed.data + (size_t) tok * d_model,
+               (size_t) d_model * sizeof(float));
+    }
+    int rc = -1;
+    bitmamba_block_t *b0 = &m->layers[0];
+    if (!batch_proj(api, ctx, BM_HIP_BUF_X, d_model, &b0->in_proj,
+                    &b0->in_proj_norm, BM_HIP_BUF_PROJ))
+        goto done;
+    api->submit_and_wait(ctx);
+    for (int i = 0; i < n_layers; i++) {
+        bitmamba_block_t *b = &m->layers[i];
+        for (int t = 0; t < n; t++)
+            block_ssm_scan(b, proj + (size_t) t * b->in_proj.rows,
+                           y + (size_t) t * d_inner);
+        if (!batch_proj(api, ctx, BM_HIP_BUF_Y, d_inner, &b->out_proj,
+                        &b->out_proj_norm, BM_HIP_BUF_OUT))
+            goto done;
+        api->encode_residual(ctx, n * d_model);
+        if (i + 1 < n_layers) {
+            bitmamba_block_t *nb = &m->layers[i + 1];
+            if (!batch_proj(api, ctx, BM_HIP_BUF_X, d_model, &nb->in_proj,
+                            &nb->in_proj_norm, BM_HIP_BUF_PROJ))
+                goto done;
+        }
+        api->submit_and_wait(ctx);
+    }
+    rc = 0;
+done:
+    api->end(ctx);
+    return rc;
+}

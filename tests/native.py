@@ -82,6 +82,7 @@ _REF_SIGS = {
     "bmref_model_set_layer_state": (None, [_vp, _i, _vp, _vp, _i]),
     "bmref_kernels_name": (C.c_char_p, []),
     "bmref_model_image": (_i, [_vp, C.POINTER(_vp), C.POINTER(_sz)]),
+    "bmref_model_prefill_batch": (_i, [_vp, _vp, _i, _vp]),
 }
 
 _oracle = None
