@@ -548,7 +548,8 @@ __global__ __launch_bounds__(256) void k_gemv_mt(const uint8_t* __restrict__ act
 }
 
 // ---------------------------------------------------------------------------
-// Few-token product on int8 MFMA (2 <= M <= 256, K % 128 == 0): block row
+// Few-token product on int8 MFMA (2 <= M <= 256, K % 128 == 0; up to 16
+// tokens at K <= 8192 go to k_gemm_few below instead): block row
 // y takes tokens 32y .. 32y+31, the 32 rows of v_mfma_i32_32x32x32_i8's A
 // operand (rows past M are not stored); 32 weight rows are its B operand.
 // A block of 8 waves owns GPB groups of 32 weight rows; the WPG waves of a
@@ -1610,15 +1611,15 @@ static hipError_t gemm_t(const uint8_t* act, const float* scale_x, int M, const 
   return hipGetLastError();
 }
 
-// which kernel serves a product of this shape
-// blocks of one k_gemm_small launch
+// blocks of one k_gemm_small (or k_gemm_few) launch
 static long long small_blocks(int M, int N, int K) {
   const int gpb = 8 / sm_wpg(slices_of(K));
   return (long long)((N + 32 * gpb - 1) / (32 * gpb)) * ((M + kSmMaxM - 1) / kSmMaxM);
 }
 
 // which kernel serves a product of this shape: 0 generic, 1 GEMV per token,
-// 2 MFMA GEMM, 3 few-token MFMA.  Few tokens: up to 32 always; up to 256
+// 2 MFMA GEMM, 3 few-token MFMA (k_gemm_few for up to 16 tokens at
+// K <= 8192, else k_gemm_small).  Few tokens: up to 32 always; up to 256
 // while one launch fits one block per CU, where it measured faster than the
 // 128-row GEMM tiles (K=4096 -> 2048: 9-11 us against 23 us at M = 32-256;
 // K=2048 -> 8384: 9.5 us against 14 us at M = 32, 64)
