@@ -66,3 +66,19 @@ def test_synth_image_size_matches_bit2_layout():
     layer = (fl(1, dm) + tern(2 * di + 3 * nh, dm) + fl(2, di * 4) + fl(1, di) + 2 * fl(1, nh)
              + 2 * fl(1, di) + tern(dm, di))
     assert blob.nbytes == 20 + fl(2, V * dm) + 2 * layer + 2 * fl(1, dm) + tern(V, dm)
+
+
+def test_batch_context_null_handling():
+    """The batch context's entry points (src/metal/bm_metal.h:57-99) on a
+    NULL context do nothing and refuse, and bm_hip_batch_begin returns NULL
+    while the backend is not initialized (no GPU here), as Metal's does
+    before bm_metal_init; none of these calls touches the GPU."""
+    L = bh.lib()
+    assert L.bm_hip_batch_ptr(None, 0) is None
+    assert not L.bm_hip_encode_bitlinear(None, 0, 64, None, 8, 64, 1.0, None, 1)
+    L.bm_hip_encode_residual(None, 16)
+    L.bm_hip_submit_and_wait(None)
+    L.bm_hip_batch_end(None)
+    if not L.bm_hip_available():
+        assert L.bm_hip_batch_begin(4, 64, 128, 128, 160) is None
+        assert "not initialized" in bh.last_error()
