@@ -301,8 +301,8 @@ def test_prefill_lengths_vs_oracle(hip):
     m = bh.Model(blob)
     O, h = _oracle_model(blob)
     try:
-        for parts in ([1], [2], [3], [5], [300], [600], [100, 200], [1, 2, 257], [1025],
-                      [2050], [7, 1030]):
+        for parts in ([1], [2], [3], [5], [12], [16], [300], [600], [100, 200], [1, 2, 257],
+                      [1025], [2050], [7, 1030]):
             note("prefill parts %s" % parts)
             m.reset()
             O.orc_model_free(h)
